@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Benchmark of the causal FlashAttention-2 fwd+bwd hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu]
+
+A step = one forward + one backward (dQ, dK, dV) of causal attention over the
+configuration's synthetic batch, through the drop-in ops (fa_fwd / fa_bwd) on
+inputs already resident in HBM.  The default workload is the benchmark's
+configuration 2: B=8, H=12, S=4096, D=64, fp16, Q/K/V N(0,1)*0.5 with RoPE.
+
+Printed (one JSON line): whole-job TFLOP/s with flops = 7*B*H*S^2*D per step
+(fwd 2 + bwd 5 causal-halved units), its fraction of the MI355X fp16 dense
+MFMA peak, a roofline object for the dominant kernel (per-launch average from
+HIP events recorded around each kernel launch on the launch stream), and the
+host-CPU baseline: the reference's own fallback call
+F.scaled_dot_product_attention(..., is_causal=True) fwd+bwd in fp32.
+Parity (sampled heads vs SDPA math fp32) runs first; a failure blocks the
+report.
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "universal-lm-trainer_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "causal FA fwd+bwd TFLOP/s & % fp16 MFMA peak, D=64 S=4096 (1 GPU)"
+PEAK_TFLOPS = 256 * 4096 * 2.4e9 / 1e12      # 2516.6: 256 CUs x 4096 flop/clk x 2.4 GHz
+HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="2", help="2, 3-512, 3-1024, 3-2048, 3-4096 or 4")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
+    ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
+    return ap.parse_args()
+
+
+def cfg_key(name):
+    return int(name) if name.isdigit() else name
+
+
+def parity_gate(ext, q, k, v, do, heads):
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    o, lse = ext.fa_fwd(q, k, v, 0.0, True, 0.125, 0)
+    dq, dk, dv = ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, 0.125, 0, 7)
+    worst = {"o_maxabs": 0.0, "dq_rel": 0.0, "dk_rel": 0.0, "dv_rel": 0.0}
+    for b, h in heads:
+        sl = lambda t: t[b:b + 1, h:h + 1].float().contiguous()
+        tq, tk, tv = (sl(t).requires_grad_(True) for t in (q, k, v))
+        with sdpa_kernel(SDPBackend.MATH):
+            ro = F.scaled_dot_product_attention(tq, tk, tv, is_causal=True, scale=0.125)
+        ro.backward(sl(do))
+        worst["o_maxabs"] = max(worst["o_maxabs"], (sl(o) - ro).abs().max().item())
+        for name, got, ref in (("dq_rel", dq, tq.grad), ("dk_rel", dk, tk.grad), ("dv_rel", dv, tv.grad)):
+            e = ((sl(got) - ref).norm() / ref.norm()).item()
+            worst[name] = max(worst[name], e)
+    ok = worst["o_maxabs"] <= 2e-3 and max(worst["dq_rel"], worst["dk_rel"], worst["dv_rel"]) <= 1e-2
+    return ok, worst
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(REPO, "profiles", "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) >= 4 and parts[0] == "traffic" and parts[1] == kernel:
+            return float(parts[2]) + float(parts[3])
+    return None
+
+
+def cpu_baseline():
+    """The reference's CPU path (train.py:1956-1961): SDPA fwd + .backward(dO)
+    in fp32 with the default CPU dispatch, on a bounded sample."""
+    import torch
+    import torch.nn.functional as F
+    import fa2_workloads as wl
+    cores = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit():
+        cores = min(cores, int(omp))
+    torch.set_num_threads(cores)
+
+    def step(q, k, v, do):
+        q, k, v = (t.detach().requires_grad_(True) for t in (q, k, v))
+        o = F.scaled_dot_product_attention(q, k, v, attn_mask=None, dropout_p=0.0, is_causal=True)
+        o.backward(do)
+
+    # configuration 1 in full: median of 10 after 2 warm-ups
+    q, k, v, do = wl.config_inputs(1)
+    for _ in range(2):
+        step(q, k, v, do)
+    ts = []
+    for _ in range(10):
+        t0 = time.perf_counter()
+        step(q, k, v, do)
+        ts.append(time.perf_counter() - t0)
+    c1_ms = statistics.median(ts) * 1e3
+    f1, b1 = wl.causal_flops(2, 4, 256)
+    # configuration-2 shape, B=1 slice (fp32), one warm-up + one timed run; scaled by B
+    q, k, v, do = (t[:1].float() for t in wl.config_inputs(2))
+    step(q, k, v, do)
+    t0 = time.perf_counter()
+    step(q, k, v, do)
+    c2_s = time.perf_counter() - t0
+    f2, b2 = wl.causal_flops(1, 12, 4096)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round((f2 + b2) / c2_s / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "reference",
+        "sample": (f"reference fallback F.scaled_dot_product_attention(is_causal=True) fwd+.backward, fp32, "
+                   f"default CPU dispatch, torch {torch.__version__}; B=1 slice of config 2 "
+                   f"(H=12 S=4096 D=64): {c2_s * 1e3:.0f} ms per fwd+bwd, value = that slice's causal "
+                   f"flops / time (whole config 2 = 8x the time); config 1 (B=2 H=4 S=256): "
+                   f"{c1_ms:.2f} ms median of 10 = {(f1 + b1) / (c1_ms / 1e3) / 1e12:.4f} TFLOP/s; "
+                   f"CPU: {cpu_model}"),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus "
+              f"{args.gpus}, WORLD_SIZE={world}); attention shards over (batch, head) with no exchange, "
+              f"so the per-GPU number is the single-GPU one.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import flash_attn_v100_cuda as fa
+    import fa2_capi
+    import fa2_workloads as wl
+
+    if not fa.is_available():
+        raise SystemExit(f"native extension not loaded: {fa.build_error()}")
+    ext = fa.extension()
+    key = cfg_key(args.config)
+    cfg = wl.CONFIGS[key]
+    B, H, S = cfg["B"], cfg["H"], cfg["S"]
+    dev = "cuda"
+    q, k, v, do = wl.config_inputs(key, device=dev)
+    torch.cuda.synchronize()
+
+    parity = None
+    if not args.no_parity:
+        ok, parity = parity_gate(ext, q, k, v, do, [(0, 0), (B - 1, H - 1)])
+        print(f"parity {parity} {'ok' if ok else 'FAILED'}", file=sys.stderr, flush=True)
+        if not ok:
+            raise SystemExit("parity gate failed: no performance report")
+
+    fwd_flops, bwd_flops = wl.causal_flops(B, H, S)
+    step_flops = fwd_flops + bwd_flops
+    scale = 0.125
+
+    def step():
+        o, lse = ext.fa_fwd(q, k, v, 0.0, True, scale, 0)
+        ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, scale, 0, 7)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+    value = step_flops * args.steps / elapsed / 1e12
+
+    # Per-kernel launch durations: HIP events around each C-ABI launch on the
+    # current stream (the stream the kernels run on), over K further steps.
+    lib = fa2_capi.load()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=dev)
+    dq, dk, dv = (torch.empty(B, H, S, 64, dtype=torch.float16, device=dev) for _ in range(3))
+    ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    pf = fa2_capi.fwd_params(q, k, v, o, lse, scale)
+    pb = fa2_capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, scale)
+    n = max(args.steps, 5)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
+    for i in range(n + 2):
+        e = ev[i - 2] if i >= 2 else None
+        if e: e[0].record(stream)
+        assert lib.fa2_fwd_f16(ctypes.byref(pf), sp) == 0, lib.fa2_last_error()
+        if e: e[1].record(stream)
+        assert lib.fa2_bwd_f16(ctypes.byref(pb), 2, ws.data_ptr(), ws.numel() * 4, sp) == 0
+        if e: e[2].record(stream)
+        assert lib.fa2_bwd_f16(ctypes.byref(pb), 4, ws.data_ptr(), ws.numel() * 4, sp) == 0
+        if e: e[3].record(stream)
+    torch.cuda.synchronize()
+    avg = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev)
+           for j, name in enumerate(("fwd", "bwd_dq", "bwd_dkv"))}
+    unit = B * H * S * S * 64
+    executed = {"fwd": 2 * unit, "bwd_dq": 3 * unit, "bwd_dkv": 4 * unit}
+    dom = max(avg, key=avg.get)
+    achieved = executed[dom] / (avg[dom] / 1e3) / 1e12
+    kernels = {kname: {"avg_ms": round(avg[kname], 4), "executed_gflop": round(executed[kname] / 1e9, 2),
+                       "tflops": round(executed[kname] / (avg[kname] / 1e3) / 1e12, 1)} for kname in avg}
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": f"causal FA-2 fwd+bwd, config {args.config}: B={B} H={H} S={S} D=64 fp16"
+                               + (" RoPE inputs" if cfg["rope"] else ""),
+                   "B": B, "H": H, "S": S, "D": 64, "algorithmic_gflop_per_step": round(step_flops / 1e9, 2)},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": round(PEAK_TFLOPS, 1),
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(dom)},
+        "kernels": kernels,
+        "parity": parity,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,128 @@
+/*
+ * fa2_mi355x.h -- C ABI of the MI355X (gfx950) causal FlashAttention-2 library.
+ *
+ * Plain C: pointers, sizes and element strides only; no torch or HIP types in
+ * the signatures (streams are passed as `void*`, i.e. a hipStream_t, NULL =
+ * the null stream).  Every entry point
+ *   - validates its arguments and returns a status code (0 = success),
+ *   - allocates nothing (outputs and workspace belong to the caller),
+ *   - launches asynchronously on the given stream and never synchronises,
+ *   - keeps no state between calls, so it is reentrant and may be called from
+ *     any host thread (the autograd engine calls the backward from its own
+ *     device thread).
+ *
+ * Tensor convention (the reference's): a 4-D fp16 tensor [B, H, S, D] with
+ * D == 64, the last dimension contiguous, and arbitrary element strides for
+ * (b, h, s).  Strides must be multiples of 8 elements and base pointers
+ * 16-byte aligned (the kernels move 16-byte vectors); the reference demands
+ * 32 bytes (reference @ None: flash_attn_v100_cuda.py:97-102), so every
+ * tensor it accepts is accepted here.
+ */
+#ifndef FA2_MI355X_H
+#define FA2_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA2_HEAD_DIM 64
+
+/* Status codes. */
+enum fa2_status {
+    FA2_OK = 0,
+    FA2_ERR_NULL_POINTER = 1,   /* a required pointer is NULL                 */
+    FA2_ERR_BAD_SHAPE = 2,      /* B/H/S negative, D != 64, int32 overflow   */
+    FA2_ERR_MISALIGNED = 3,     /* pointer or stride breaks 16-byte alignment */
+    FA2_ERR_BAD_ARGUMENT = 4,   /* dropout_p outside [0,1), bad mode bits ... */
+    FA2_ERR_WORKSPACE = 5,      /* workspace missing or too small            */
+    FA2_ERR_LAUNCH = 6          /* the HIP runtime rejected a kernel launch   */
+};
+
+/* Forward: O = softmax(scale * Q K^T [+ causal mask]) V, with dropout on P,
+ * and LSE[b,h,i] = natural-log logsumexp of row i of the scaled, masked
+ * scores (-inf for a row with no visible key).
+ * Replaces fav100::fa_fwd / fa_fwd_kernel
+ *   (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:40-364). */
+typedef struct fa2_fwd_params {
+    const void *q, *k, *v;          /* fp16 [B,H,S,64]                         */
+    void *o;                        /* fp16 [B,H,S,64] output                  */
+    float *lse;                     /* fp32 [B,H,S] output                     */
+    int64_t q_stride[3], k_stride[3], v_stride[3], o_stride[3]; /* b,h,s     */
+    int64_t lse_stride[2];          /* b,h (the s stride is 1)                 */
+    int32_t B, H, S, D;
+    float softmax_scale;            /* the reference default is D^-0.5         */
+    float dropout_p;                /* 0 <= p < 1                              */
+    uint32_t seed;                  /* dropout hash seed                       */
+    int32_t causal;                 /* nonzero: key j visible to query i iff j <= i */
+} fa2_fwd_params;
+
+int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
+
+/* Backward: dQ, dK, dV from Q, K, V, O, LSE and dO, recomputing P from LSE.
+ * delta[b,h,i] = sum_d O*dO (fp32) is produced inside the dQ pass and kept in
+ * the workspace for the dK/dV pass.
+ * Replaces fav100::fa_bwd and its three kernels (delta, dQ, dK/dV)
+ *   (reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:42-506).
+ * `mode` keeps the reference's bit mask (bwd.cu:476-502):
+ *   bit 1 = delta, bit 2 = dQ, bit 4 = dK/dV; 7 = all.  Here delta is fused
+ *   into the dQ pass, so bit 1 alone computes delta only, bit 2 computes delta
+ *   and dQ, and bit 4 without bit 1 or 2 reads delta left in the workspace by
+ *   an earlier call. */
+typedef struct fa2_bwd_params {
+    const void *q, *k, *v, *o, *dout;   /* fp16 [B,H,S,64]                     */
+    const float *lse;                   /* fp32 [B,H,S] from the forward       */
+    void *dq, *dk, *dv;                 /* fp16 [B,H,S,64] outputs             */
+    int64_t q_stride[3], k_stride[3], v_stride[3], o_stride[3], do_stride[3];
+    int64_t dq_stride[3], dk_stride[3], dv_stride[3];
+    int64_t lse_stride[2];
+    int32_t B, H, S, D;
+    float softmax_scale;
+    float dropout_p;
+    uint32_t seed;
+    int32_t causal;
+} fa2_bwd_params;
+
+/* Workspace bytes fa2_bwd_f16 needs for (B, H, S): the fp32 delta rows. */
+size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S);
+
+int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,
+                size_t workspace_bytes, void *stream);
+
+/* Fused rotary embedding on q and k (head_dim 64), fp32 arithmetic with one
+ * fp16 rounding, no fused multiply-add (bitwise equal to the eager fp32 path
+ * followed by .half()):
+ *   forward : out[d] = x[d]*cos[d] + r[d]*sin[d],  r[d] = -x[d+32] (d<32),
+ *                                                       x[d-32]  (d>=32)
+ *   backward: gx[d]  = g[d]*cos[d] + t[d],         t[d] = +g[d+32]*sin[d+32] (d<32),
+ *                                                       -g[d-32]*sin[d-32] (d>=32)
+ * cos/sin are fp32 [S,64] with row stride cs_stride/sn_stride.
+ * Replaces fastops::rope_fwd / rope_bwd
+ *   (reference @ None: csrc/flash_attn_v100/fast_ops.cu:31-216).
+ * q/k/outputs need 4-byte alignment and even strides only. */
+typedef struct fa2_rope_params {
+    const void *q, *k;              /* fp16 [B,H,S,64] inputs (grads in bwd)   */
+    void *qo, *ko;                  /* fp16 [B,H,S,64] outputs                 */
+    const float *cos, *sin;         /* fp32 [S,64]                             */
+    int64_t q_stride[3], k_stride[3], qo_stride[3], ko_stride[3];
+    int64_t cs_stride, sn_stride;
+    int32_t B, H, S, D;
+} fa2_rope_params;
+
+int fa2_rope_f16(const fa2_rope_params *p, int32_t backward, void *stream);
+
+/* Human-readable text for a status code, and the detail message of the last
+ * failing call on this host thread ("" if none). */
+const char *fa2_status_string(int status);
+const char *fa2_last_error(void);
+
+/* Library version string and the gfx target the kernels were built for. */
+const char *fa2_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA2_MI355X_H */

@@ -1,0 +1,263 @@
+"""GPU parity of the gfx950 kernels (run on the MI355X box).
+
+Bars (from the benchmark definition): O max-abs <= 2e-3 against the
+reference's own path (SDPA math in fp32/fp64 on the same fp16 inputs), and
+dQ/dK/dV relative error <= 1e-2 (relative L2 norm; max-abs is printed too).
+Small shapes are checked against the fp64 CPU oracle and the committed golden
+fixtures; the benchmark's full shapes are checked on sampled heads against
+SDPA math in fp32 on the GPU plus size-independent properties.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+import fa2_capi as capi
+import fa2_workloads as wl
+from oracle import fa2_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+O_TOL = 2e-3
+G_TOL = 1e-2
+LSE_TOL = 1e-3
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fa2_golden.npz")
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def run_kernel(fa, q, k, v, do, causal=True, scale=0.125, p=0.0, seed=0):
+    ext = fa.extension()
+    o, lse = ext.fa_fwd(q, k, v, p, causal, scale, seed)
+    dq, dk, dv = ext.fa_bwd(q, k, v, o, lse, do, p, causal, scale, seed, 7)
+    torch.cuda.synchronize()
+    return o, lse, dq, dk, dv
+
+
+def check_against(name, got, ref):
+    o, lse, dq, dk, dv = (t.detach().float().cpu().numpy() for t in got)
+    ro, rlse, rdq, rdk, rdv = (np.asarray(x, np.float64) for x in ref)
+    eo = orc.max_abs(o, ro)
+    el = orc.max_abs(lse, rlse)
+    eg = [orc.rel_l2(a, b) for a, b in ((dq, rdq), (dk, rdk), (dv, rdv))]
+    ma = [orc.max_abs(a, b) for a, b in ((dq, rdq), (dk, rdk), (dv, rdv))]
+    say(f"{name}: O maxabs {eo:.2e}  LSE maxabs {el:.2e}  rel dQ/dK/dV {eg[0]:.2e} {eg[1]:.2e} {eg[2]:.2e}"
+        f"  maxabs {ma[0]:.2e} {ma[1]:.2e} {ma[2]:.2e}")
+    assert eo <= O_TOL, f"{name}: O max-abs {eo}"
+    assert el <= LSE_TOL, f"{name}: LSE max-abs {el}"
+    for e, n in zip(eg, ("dQ", "dK", "dV")):
+        assert e <= G_TOL, f"{name}: {n} rel err {e}"
+
+
+def oracle_ref(q, k, v, do, causal, scale, p=0.0, seed=0):
+    qn, kn, vn, don = (t.detach().float().cpu().numpy() for t in (q, k, v, do))
+    keep = orc.keep_mask(seed, q.shape[0], q.shape[1], q.shape[2], p) if p > 0 else None
+    o, lse = orc.attention_dense_fwd(qn, kn, vn, causal=causal, scale=scale, keep=keep, p=p)
+    dq, dk, dv, _ = orc.attention_bwd(qn, kn, vn, o, lse, don, causal=causal, scale=scale, keep=keep, p=p)
+    return o, lse, dq, dk, dv
+
+
+def sdpa_ref_gpu(q, k, v, do, causal=True, scale=0.125):
+    """The reference's fallback path (SDPA, MATH backend) in fp32 on the GPU."""
+    tq, tk, tv = (t.detach().float().contiguous().requires_grad_(True) for t in (q, k, v))
+    with sdpa_kernel(SDPBackend.MATH):
+        o = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal, scale=scale)
+    o.backward(do.float().contiguous())
+    s = torch.matmul(tq.detach(), tk.detach().transpose(-1, -2).contiguous()) * scale
+    if causal:
+        S = q.shape[-2]
+        s.masked_fill_(torch.ones(S, S, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    return [t.detach().double().cpu().numpy() for t in (o, lse, tq.grad, tk.grad, tv.grad)]
+
+
+def rand_inputs(B, H, S, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(B, H, S, 64, generator=g) * scale).half().to(DEV) for _ in range(4)]
+
+
+@pytest.mark.parametrize("S", [1, 2, 17, 63, 64, 65, 127, 129, 200, 256, 257, 300, 513])
+@pytest.mark.parametrize("causal", [True, False])
+def test_small_shapes_vs_oracle(fa, S, causal):
+    say(f"case small S={S} causal={causal}")
+    q, k, v, do = rand_inputs(1, 2, S, seed=S + 1000 * causal)
+    got = run_kernel(fa, q, k, v, do, causal=causal)
+    check_against(f"S={S} causal={causal}", got, oracle_ref(q, k, v, do, causal, 0.125))
+
+
+def test_golden_fixtures(fa):
+    z = np.load(GOLDEN)
+    names = sorted({k.split("/")[0] for k in z.files if not k.startswith("mask")})
+    for name in names:
+        B, H, S, causal, scale, p, seed = z[f"{name}/meta"]
+        say(f"case golden {name}")
+        q, k, v, do = (torch.from_numpy(z[f"{name}/{t}"]).to(DEV) for t in ("q", "k", "v", "do"))
+        got = run_kernel(fa, q, k, v, do, causal=bool(causal), scale=float(scale), p=float(p), seed=int(seed))
+        ref = [z[f"{name}/{t}"] for t in ("o", "lse", "dq", "dk", "dv")]
+        check_against(f"golden {name}", got, ref)
+
+
+@pytest.mark.parametrize("scale", [0.3, -0.2, 0.0, 0.05])
+def test_softmax_scales(fa, scale):
+    say(f"case scale={scale}")
+    q, k, v, do = rand_inputs(1, 2, 190, seed=77)
+    got = run_kernel(fa, q, k, v, do, scale=scale)
+    check_against(f"scale={scale}", got, oracle_ref(q, k, v, do, True, scale))
+
+
+@pytest.mark.parametrize("p,seed", [(0.1, 1), (0.5, 0xC0FFEE), (0.9, 42)])
+def test_dropout_vs_oracle(fa, p, seed):
+    say(f"case dropout p={p} seed={seed}")
+    q, k, v, do = rand_inputs(2, 2, 160, seed=seed % 1000)
+    got = run_kernel(fa, q, k, v, do, p=p, seed=seed)
+    check_against(f"dropout p={p}", got, oracle_ref(q, k, v, do, True, 0.125, p=p, seed=seed))
+
+
+def test_medium_vs_sdpa_math_gpu(fa):
+    say("case medium B=2 H=4 S=1024 vs SDPA math fp32")
+    q, k, v, do = rand_inputs(2, 4, 1024, seed=5)
+    got = run_kernel(fa, q, k, v, do)
+    check_against("medium", got, sdpa_ref_gpu(q, k, v, do))
+
+
+def test_train_py_layouts_are_bitwise_identical(fa):
+    """q/k as dense [B,S,H,D] views, v a view of the fused qkv tensor, dO the
+    transposed view of a [B,S,H,D] grad: same bits as contiguous inputs."""
+    say("case train.py layouts")
+    B, S, H = 2, 333, 12
+    g = torch.Generator().manual_seed(9)
+    qkv = torch.randn(B, S, 3 * H * 64, generator=g).half().to(DEV)
+    q, k, v = qkv.chunk(3, dim=-1)
+    q = q.view(B, S, H, 64).transpose(1, 2)
+    k = k.contiguous().view(B, S, H, 64).transpose(1, 2)
+    v = v.view(B, S, H, 64).transpose(1, 2)
+    do = torch.randn(B, S, H, 64, generator=g).half().to(DEV).transpose(1, 2)
+    assert v.stride(2) == 3 * H * 64 and not do.is_contiguous()
+    got = run_kernel(fa, q, k, v, do)
+    ref = run_kernel(fa, *(t.contiguous() for t in (q, k, v, do)))
+    for a, b, n in zip(got, ref, ("o", "lse", "dq", "dk", "dv")):
+        assert torch.equal(a, b), n
+
+
+def test_autograd_wrapper_and_sdpa_shim(fa):
+    say("case autograd wrapper")
+    q, k, v, do = rand_inputs(1, 3, 300, seed=11)
+    qs, ks, vs = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = fa.flash_attn_v100(qs, ks, vs)
+    out.backward(do)
+    got = run_kernel(fa, q, k, v, do)
+    assert torch.equal(out.detach(), got[0])
+    for a, b in zip((qs.grad, ks.grad, vs.grad), got[2:]):
+        assert torch.equal(a, b)
+    shim = fa.sdpa(q, k, v, is_causal=True)
+    assert torch.equal(shim, got[0])
+    masked = fa.sdpa(q.float(), k.float(), v.float(), is_causal=True)   # fp32 -> SDPA fallback
+    assert masked.dtype == torch.float32
+
+
+def test_capi_direct_matches_binding(fa):
+    """Call fa2_fwd_f16 / fa2_bwd_f16 through ctypes on torch's current stream."""
+    say("case C ABI direct")
+    lib = capi.load()
+    q, k, v, do = rand_inputs(2, 3, 200, seed=21)
+    B, H, S, _ = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = capi.fwd_params(q, k, v, o, lse, 0.125)
+    assert lib.fa2_fwd_f16(ctypes.byref(p), stream) == 0, lib.fa2_last_error()
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4, device=DEV)
+    pb = capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, 0.125)
+    assert lib.fa2_bwd_f16(ctypes.byref(pb), 7, ws.data_ptr(), ws.numel() * 4, stream) == 0
+    torch.cuda.synchronize()
+    ref = run_kernel(fa, q, k, v, do)
+    for a, b in zip((o, lse, dq, dk, dv), ref):
+        assert torch.equal(a, b)
+    # delta left in the workspace equals rowsum(O * dO)
+    delta = (o.float() * do.float()).sum(-1).reshape(-1)
+    assert torch.allclose(ws[: B * H * S], delta, atol=1e-3, rtol=1e-3)
+
+
+def test_deterministic(fa):
+    say("case determinism")
+    q, k, v, do = rand_inputs(2, 4, 777, seed=3)
+    a = run_kernel(fa, q, k, v, do)
+    b = run_kernel(fa, q, k, v, do)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def _check_sampled_heads(fa, name, q, k, v, do, heads):
+    got = run_kernel(fa, q, k, v, do)
+    o, lse, dq, dk, dv = got
+    for t in got:
+        assert torch.isfinite(t).all(), name
+    # p = 0: rows of P sum to 1, so the dV rows sum to the dO rows per head.
+    sdv = dv.float().sum(dim=2)
+    sdo = do.float().sum(dim=2)
+    err = (sdv - sdo).abs().max().item() / max(1.0, sdo.abs().max().item())
+    say(f"{name}: sum-rows(dV) vs sum-rows(dO) rel {err:.2e}")
+    assert err < 1e-2
+    for b, h in heads:
+        sl = lambda t: t[b:b + 1, h:h + 1]
+        ref = sdpa_ref_gpu(sl(q), sl(k), sl(v), sl(do))
+        check_against(f"{name} b={b} h={h}", [sl(t) for t in got], ref)
+
+
+def test_config2_full_shape(fa):
+    say("case config 2 full shape B=8 H=12 S=4096 (RoPE inputs)")
+    q, k, v, do = wl.config_inputs(2, device=DEV)
+    _check_sampled_heads(fa, "config2", q, k, v, do, [(0, 0), (7, 11), (3, 5)])
+
+
+@pytest.mark.parametrize("S", [512, 1024, 2048])
+def test_config3_buckets(fa, S):
+    say(f"case config 3 S={S}")
+    q, k, v, do = wl.config_inputs(f"3-{S}", device=DEV)
+    _check_sampled_heads(fa, f"config3-{S}", q, k, v, do, [(0, 0), (q.shape[0] - 1, 11)])
+
+
+def test_config4_outlier_rows(fa):
+    say("case config 4 B=8 H=16 S=4096 with x8 rows")
+    q, k, v, do = wl.config_inputs(4, device=DEV)
+    norms = q.float().norm(dim=-1)                       # [B,H,S]
+    b, h = divmod(int(norms.amax(dim=2).flatten().argmax()), q.shape[1])  # head holding the largest row
+    _check_sampled_heads(fa, "config4", q, k, v, do, [(b, h), (0, 0)])
+
+
+def test_rope_bitwise_vs_oracle(fa):
+    say("case rope fwd/bwd bitwise")
+    B, S, H = 2, 257, 12
+    g = torch.Generator().manual_seed(4)
+    qkv = torch.randn(B, S, 3 * H * 64, generator=g).half()
+    q, k, _ = qkv.chunk(3, dim=-1)
+    q = q.view(B, S, H, 64).transpose(1, 2)
+    k = k.view(B, S, H, 64).transpose(1, 2)
+    cos, sin = wl.rope_tables(S)
+    cos_pad = torch.zeros(S, 128)
+    cos_pad[:, :64] = cos                     # row-padded view like cos_cached[..., :64]
+    sin_pad = torch.zeros(S, 128)
+    sin_pad[:, :64] = sin
+    c2, s2 = cos_pad.to(DEV)[:, :64], sin_pad.to(DEV)[:, :64]
+    qd, kd = q.to(DEV), k.to(DEV)
+    assert fa.rope_can_use(qd, kd, c2, s2)
+    qo, ko = fa.rope(qd, kd, c2, s2)
+    torch.cuda.synchronize()
+    for got, x in ((qo, q), (ko, k)):
+        ref = orc.rope_fwd(x.numpy(), cos.numpy(), sin.numpy())
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+    gq = torch.randn(B, H, S, 64, generator=g).half()
+    gk = torch.randn(B, H, S, 64, generator=g).half()
+    dq, dk = fa.extension().rope_bwd(gq.to(DEV), gk.to(DEV), c2, s2, qd, kd)
+    torch.cuda.synchronize()
+    for got, gg in ((dq, gq), (dk, gk)):
+        ref = orc.rope_bwd(gg.numpy(), cos.numpy(), sin.numpy())
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))

@@ -1,0 +1,206 @@
+"""Host-side checks that need no GPU: the C library loads and exports every
+function of include/fa2_mi355x.h, the ctypes mirror matches the C struct
+layout, argument validation rejects bad calls before touching the device, and
+the Python drop-in module keeps the reference's API, eligibility predicate
+and fallback behaviour (reference @ None: flash_attn_v100_cuda.py:59-166,
+train.py:87-113, 1946-1961)."""
+import ctypes
+import os
+import subprocess
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import fa2_capi as capi
+
+REPO = capi.REPO
+
+
+def test_library_exports_every_header_function():
+    lib = capi.load()
+    names = capi.header_functions()
+    assert set(names) >= {"fa2_fwd_f16", "fa2_bwd_f16", "fa2_bwd_workspace_bytes", "fa2_rope_f16",
+                          "fa2_status_string", "fa2_last_error", "fa2_version"}
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    assert b"gfx950" in lib.fa2_version()
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """Compile the header with gcc and compare sizeof/offsetof with ctypes."""
+    src = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{capi.HEADER}"', "int main(void){"]
+    for cname, cls in capi.STRUCTS.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0;}")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(src)], check=True)
+    out = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                        text=True).stdout.split("\n") if l)
+    for cname, cls in capi.STRUCTS.items():
+        assert int(out[cname]) == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert int(out[f"{cname}.{fname}"]) == getattr(cls, fname).offset, f"{cname}.{fname}"
+
+
+def _dummy_fwd(**kw):
+    p = capi.FwdParams()
+    base = 1 << 20  # never dereferenced: every case fails validation first
+    p.q = p.k = p.v = p.o = p.lse = base
+    for f in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        setattr(p, f, capi.I64x3(64 * 8 * 16, 64 * 16, 64))
+    p.lse_stride = capi.I64x2(8 * 16, 16)
+    p.B, p.H, p.S, p.D = 2, 8, 16, 64
+    p.softmax_scale, p.dropout_p, p.seed, p.causal = 0.125, 0.0, 0, 1
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("D", 128, 2), ("S", -1, 2), ("q", 0, 1), ("lse", 0, 1), ("k", (1 << 20) + 8, 3),
+    ("v_stride", capi.I64x3(64 * 8 * 16, 64 * 16, 68), 3), ("dropout_p", 1.0, 4),
+    ("dropout_p", -0.1, 4), ("softmax_scale", float("nan"), 4),
+])
+def test_fwd_validation_rejects_before_launch(field, value, status):
+    lib = capi.load()
+    p = _dummy_fwd(**{field: value})
+    rc = lib.fa2_fwd_f16(ctypes.byref(p), None)
+    assert rc == status, (rc, lib.fa2_last_error())
+    assert lib.fa2_last_error() != b""
+    assert lib.fa2_status_string(rc) != b"unknown status"
+
+
+def test_empty_problem_is_a_noop():
+    lib = capi.load()
+    for dim in ("B", "H", "S"):
+        p = _dummy_fwd(**{dim: 0})
+        assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 0
+    assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 2 * 3 * 5 * 4
+    assert lib.fa2_bwd_workspace_bytes(0, 3, 5) == 0
+
+
+def test_bwd_validation():
+    lib = capi.load()
+    p = capi.BwdParams()
+    p.B, p.H, p.S, p.D, p.softmax_scale = 1, 1, 64, 64, 0.125
+    assert lib.fa2_bwd_f16(ctypes.byref(p), 9, None, 0, None) == 4          # bad mode
+    assert lib.fa2_bwd_f16(ctypes.byref(p), 7, None, 0, None) == 5          # no workspace
+    assert lib.fa2_bwd_f16(ctypes.byref(p), 7, ctypes.c_void_p(1 << 20), 16, None) == 5  # too small
+    assert lib.fa2_bwd_f16(ctypes.byref(p), 0, None, 0, None) == 0          # nothing requested
+    assert lib.fa2_bwd_f16(None, 7, None, 0, None) == 1
+
+
+# ---------------------------------------------------------------------------
+# Python drop-in module
+# ---------------------------------------------------------------------------
+import flash_attn_v100_cuda as fa  # noqa: E402
+
+
+def test_module_api_surface():
+    for name in ("is_available", "build_error", "can_use", "flash_attn_v100", "rope_can_use", "rope",
+                 "_next_seed", "_fa_ready", "sdpa"):
+        assert callable(getattr(fa, name)), name
+
+
+def test_extension_loads_on_host():
+    assert fa.is_available(), fa.build_error()
+    ext = fa.extension()
+    for op in ("fa_fwd", "fa_bwd", "rope_fwd", "rope_bwd"):
+        assert hasattr(ext, op)
+
+
+def test_cpu_tensors_are_ineligible_and_rejected():
+    q = torch.randn(1, 2, 64, 64, dtype=torch.float16)
+    assert not fa.can_use(q, q, q)
+    with pytest.raises(ValueError):
+        fa.flash_attn_v100(q, q, q)
+    cos = torch.zeros(64, 64)
+    assert not fa.rope_can_use(q, q, cos, cos)
+
+
+def test_sdpa_shim_falls_back_bitwise_on_cpu():
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(2, 4, 256, 64, generator=g) for _ in range(3))
+    for kw in (dict(is_causal=True), dict(is_causal=False), dict(attn_mask=torch.ones(256, 256, dtype=torch.bool))):
+        ref = F.scaled_dot_product_attention(q, k, v, **kw)
+        assert torch.equal(fa.sdpa(q, k, v, **kw), ref)
+
+
+def test_disable_switch_forces_sdpa(monkeypatch):
+    monkeypatch.setenv("FA_V100_DISABLE", "1")
+    q = torch.randn(1, 1, 8, 64)
+    assert torch.equal(fa.sdpa(q, q, q, is_causal=True),
+                       F.scaled_dot_product_attention(q, q, q, is_causal=True))
+
+
+def test_missing_build_reports_and_raises(monkeypatch):
+    """A missing extension must surface as is_available()==False plus a
+    build_error() text (train.py:88-95 prints it and falls back), and the op
+    itself must raise instead of silently computing on the CPU."""
+    monkeypatch.setattr(fa, "_EXT", None)
+    monkeypatch.setattr(fa, "_BUILD_ERROR", ImportError("not built"))
+    assert not fa.is_available()
+    assert "not built" in str(fa.build_error())
+    with pytest.raises(RuntimeError):
+        fa.extension()
+    with pytest.raises(RuntimeError):
+        fa._FlashAttnV100Cuda.forward(None, None, None, None, 0.0, True, 0.125)
+
+
+def test_build_failure_path_in_fresh_process(tmp_path):
+    """Point the loader at an empty lib dir in a fresh interpreter."""
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import flash_attn_v100_cuda as fa\n"
+        "fa._LIB_DIR = %r\n"
+        "print(fa.is_available(), type(fa.build_error()).__name__)\n"
+    ) % (os.path.join(REPO, "universal-lm-trainer_amd"), str(tmp_path))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True).stdout
+    assert out.split() == ["False", "ImportError"]
+
+
+def test_eligibility_predicate_matches_reference_rules():
+    """_fa_ready: fp16, 4-D, D=64, unit last stride, 32-byte base and strides."""
+    class Fake:
+        def __init__(self, dtype=torch.float16, shape=(1, 2, 8, 64), stride=(1024, 512, 64, 1), ptr=0):
+            self.is_cuda, self.dtype, self._shape, self._stride, self._ptr = True, dtype, shape, stride, ptr
+
+        def dim(self):
+            return len(self._shape)
+
+        def size(self, i):
+            return self._shape[i]
+
+        def stride(self, i=None):
+            return self._stride if i is None else self._stride[i]
+
+        def data_ptr(self):
+            return self._ptr
+
+        @property
+        def shape(self):
+            return torch.Size(self._shape)
+
+    assert fa._fa_ready(Fake())
+    assert not fa._fa_ready(Fake(dtype=torch.float32))
+    assert not fa._fa_ready(Fake(shape=(1, 2, 8, 128), stride=(2048, 1024, 128, 1)))
+    assert not fa._fa_ready(Fake(stride=(1024, 512, 64, 2)))
+    assert not fa._fa_ready(Fake(ptr=16))
+    assert not fa._fa_ready(Fake(stride=(1024, 520, 64, 1)))   # 1040 B not 32B-aligned
+    # train.py layouts: q/k dense [B,S,H,D] view (row stride 768), v view of fused qkv (2304)
+    assert fa._fa_ready(Fake(shape=(2, 12, 16, 64), stride=(16 * 768, 64, 768, 1)))
+    assert fa._fa_ready(Fake(shape=(2, 12, 16, 64), stride=(16 * 2304, 64, 2304, 1), ptr=2 * 768 * 2))
+
+
+def test_seed_counter_formula(monkeypatch):
+    from oracle import fa2_oracle as orc
+    monkeypatch.setattr(torch.cuda, "initial_seed", lambda: 12345)
+    import itertools
+    monkeypatch.setattr(fa, "_SEED_COUNTER", itertools.count(1))
+    assert [fa._next_seed() for _ in range(3)] == [orc.next_seed(12345, i) for i in (1, 2, 3)]

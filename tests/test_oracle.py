@@ -1,0 +1,265 @@
+"""Pins the CPU oracle (oracle/fa2_oracle.py) before any GPU result is trusted.
+
+Each check is independent of the oracle's own formulas: torch's SDPA MATH
+backend and autograd (library routines), closed forms, invariants, and an
+independent integer evaluation of the dropout hash.  A mistake planted in a
+copy of the oracle (dropped delta term, wrong scale placement) is shown to
+fail the invariant checks.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from oracle import fa2_oracle as orc
+
+TAIL_SIZES = [1, 2, 17, 63, 64, 65, 127, 129, 200]
+
+
+def _rand(shape, seed, scale=1.0):
+    g = np.random.default_rng(seed)
+    return g.standard_normal(shape) * scale
+
+
+def _sdpa_math(q, k, v, causal, scale=None):
+    with sdpa_kernel(SDPBackend.MATH):
+        return F.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)
+
+
+def _lse_ref(q, k, causal, scale):
+    s = torch.einsum("bhid,bhjd->bhij", q, k) * scale
+    if causal:
+        S = q.shape[-2]
+        s = s.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    return torch.logsumexp(s, dim=-1)
+
+
+@pytest.mark.parametrize("S", TAIL_SIZES)
+@pytest.mark.parametrize("causal", [True, False])
+def test_dense_fwd_matches_sdpa_math(S, causal):
+    q, k, v = (_rand((1, 2, S, 64), 10 * S + i) for i in range(3))
+    o, lse = orc.attention_dense_fwd(q, k, v, causal=causal)
+    tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
+    ref = _sdpa_math(tq, tk, tv, causal).numpy()
+    assert orc.max_abs(o, ref) < 1e-12
+    assert orc.max_abs(lse, _lse_ref(tq, tk, causal, 0.125).numpy()) < 1e-12
+
+
+@pytest.mark.parametrize("S", TAIL_SIZES)
+def test_tiled_fwd_matches_dense(S):
+    q, k, v = (_rand((1, 2, S, 64), 7 * S + i, 2.0) for i in range(3))
+    for causal in (True, False):
+        o1, l1 = orc.attention_dense_fwd(q, k, v, causal=causal)
+        o2, l2 = orc.attention_tiled_fwd(q, k, v, causal=causal)
+        assert orc.max_abs(o1, o2) < 1e-11
+        assert orc.max_abs(l1, l2) < 1e-11
+
+
+def test_tiled_fwd_dropout_matches_dense():
+    S, p, seed = 150, 0.3, 12345
+    q, k, v = (_rand((2, 2, S, 64), 99 + i) for i in range(3))
+    keep = orc.keep_mask(seed, 2, 2, S, p)
+    o1, l1 = orc.attention_dense_fwd(q, k, v, keep=keep, p=p)
+    o2, l2 = orc.attention_tiled_fwd(q, k, v, keep=keep, p=p)
+    assert orc.max_abs(o1, o2) < 1e-11
+    assert orc.max_abs(l1, l2) < 1e-11
+
+
+def test_closed_forms():
+    S = 130
+    q, k, v = (_rand((1, 1, S, 64), 3 + i) for i in range(3))
+    # Causal row 0 sees only key 0: O_0 = V_0 exactly.
+    o, lse = orc.attention_dense_fwd(q, k, v)
+    assert orc.max_abs(o[0, 0, 0], v[0, 0, 0]) < 1e-15
+    # Q == 0: uniform weights, O_i = mean(V_0..V_i), LSE_i = ln(i+1).
+    o, lse = orc.attention_tiled_fwd(np.zeros_like(q), k, v)
+    cum = np.cumsum(v[0, 0], axis=0) / np.arange(1, S + 1)[:, None]
+    assert orc.max_abs(o[0, 0], cum) < 1e-12
+    assert orc.max_abs(lse[0, 0], np.log(np.arange(1, S + 1))) < 1e-12
+    # LSE_i >= max_j s_ij (visible j).
+    o, lse = orc.attention_dense_fwd(q, k, v)
+    s = np.einsum("id,jd->ij", q[0, 0], k[0, 0]) * 0.125
+    s = np.where(np.tril(np.ones((S, S), bool)), s, -np.inf)
+    assert np.all(lse[0, 0] >= s.max(axis=1) - 1e-12)
+
+
+@pytest.mark.parametrize("S", [1, 17, 64, 65, 129])
+@pytest.mark.parametrize("causal", [True, False])
+def test_bwd_matches_sdpa_autograd(S, causal):
+    q, k, v, do = (_rand((1, 2, S, 64), 31 * S + i) for i in range(4))
+    o, lse = orc.attention_dense_fwd(q, k, v, causal=causal)
+    dq, dk, dv, delta = orc.attention_bwd(q, k, v, o, lse, do, causal=causal)
+    tq, tk, tv = (torch.from_numpy(x).requires_grad_(True) for x in (q, k, v))
+    out = _sdpa_math(tq, tk, tv, causal)
+    out.backward(torch.from_numpy(do))
+    assert orc.max_abs(dq, tq.grad.numpy()) < 1e-11
+    assert orc.max_abs(dk, tk.grad.numpy()) < 1e-11
+    assert orc.max_abs(dv, tv.grad.numpy()) < 1e-11
+    assert orc.max_abs(delta, (o * do).sum(-1)) < 1e-12
+
+
+def test_bwd_with_scale_matches_autograd():
+    S = 77
+    q, k, v, do = (_rand((1, 2, S, 64), 500 + i) for i in range(4))
+    for scale in (0.3, -0.2):
+        o, lse = orc.attention_dense_fwd(q, k, v, scale=scale)
+        dq, dk, dv, _ = orc.attention_bwd(q, k, v, o, lse, do, scale=scale)
+        tq, tk, tv = (torch.from_numpy(x).requires_grad_(True) for x in (q, k, v))
+        out = _sdpa_math(tq, tk, tv, True, scale=scale)
+        assert orc.max_abs(o, out.detach().numpy()) < 1e-12
+        out.backward(torch.from_numpy(do))
+        for mine, ref in ((dq, tq), (dk, tk), (dv, tv)):
+            assert orc.max_abs(mine, ref.grad.numpy()) < 1e-11
+
+
+def test_bwd_dropout_matches_explicit_mask_autograd():
+    """p > 0: autograd of softmax(S) * keep/(1-p) @ V with the same keep mask."""
+    S, p, seed = 96, 0.2, 777
+    q, k, v, do = (_rand((1, 2, S, 64), 40 + i) for i in range(4))
+    keep = orc.keep_mask(seed, 1, 2, S, p)
+    o, lse = orc.attention_dense_fwd(q, k, v, keep=keep, p=p)
+    dq, dk, dv, _ = orc.attention_bwd(q, k, v, o, lse, do, keep=keep, p=p)
+    tq, tk, tv = (torch.from_numpy(x).requires_grad_(True) for x in (q, k, v))
+    s = torch.einsum("bhid,bhjd->bhij", tq, tk) * 0.125
+    s = s.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    out = torch.softmax(s, dim=-1) * torch.from_numpy(keep.astype(np.float64)) / (1 - p) @ tv
+    assert orc.max_abs(o, out.detach().numpy()) < 1e-12
+    out.backward(torch.from_numpy(do))
+    for mine, ref in ((dq, tq), (dk, tk), (dv, tv)):
+        assert orc.max_abs(mine, ref.grad.numpy()) < 1e-11
+
+
+def _invariants_hold(bwd, q, k, v, do):
+    """Rows of dS sum to 0 => dQ is unchanged when every key is shifted by
+    the same vector; rows of P sum to 1 => sum_j dV_j = sum_i dO_i."""
+    o, lse = orc.attention_dense_fwd(q, k, v)
+    dq, dk, dv, _ = bwd(q, k, v, o, lse, do)
+    shift = _rand((1, 1, 1, 64), 4242)
+    k2 = k + shift
+    o2, lse2 = orc.attention_dense_fwd(q, k2, v)
+    dq2, _, _, _ = bwd(q, k2, v, o2, lse2, do)
+    ok_shift = orc.max_abs(dq, dq2) < 1e-10
+    ok_sum = orc.max_abs(dv.sum(axis=2), do.sum(axis=2)) < 1e-10
+    return ok_shift and ok_sum
+
+
+def test_bwd_invariants_and_planted_mistakes():
+    S = 90
+    q, k, v, do = (_rand((1, 2, S, 64), 60 + i) for i in range(4))
+    assert _invariants_hold(orc.attention_bwd, q, k, v, do)
+
+    def no_delta(q, k, v, o, lse, do):  # planted mistake: dS = P*dP (delta dropped)
+        return orc.attention_bwd(q, k, v, np.zeros_like(o), lse, do)
+
+    assert not _invariants_hold(no_delta, q, k, v, do)
+
+    def wrong_lse(q, k, v, o, lse, do):  # planted mistake: P from lse off by one row
+        return orc.attention_bwd(q, k, v, o, np.roll(lse, 1, axis=-1), do)
+
+    assert not _invariants_hold(wrong_lse, q, k, v, do)
+
+
+def _keep_py(seed, row, col, bh, p):
+    """Pure-Python integer evaluation of the reference's dropout hash."""
+    M = 0xFFFFFFFF
+    h = (seed * 0x9E3779B1) & M
+    h ^= ((row + 1) * 0x85EBCA6B) & M
+    h ^= ((col + 1) * 0xC2B2AE35) & M
+    h ^= ((bh + 1) * 0x27D4EB2F) & M
+    h ^= h >> 16
+    h = (h * 0x7FEB352D) & M
+    h ^= h >> 15
+    h = (h * 0x846CA68B) & M
+    h ^= h >> 16
+    return (h >> 8) >= math.ceil(float(np.float32(p)) * 16777216.0)
+
+
+def test_dropout_hash_integer_arithmetic():
+    rng = np.random.default_rng(5)
+    for _ in range(300):
+        seed = int(rng.integers(0, 2 ** 32))
+        row, col, bh = (int(x) for x in rng.integers(0, 70000, size=3))
+        p = float(rng.choice([0.0, 0.1, 0.25, 0.5, 0.9]))
+        assert bool(orc.dropout_keep(seed, row, col, bh, p)) == _keep_py(seed, row, col, bh, p)
+
+
+def test_dropout_statistics():
+    S, p = 512, 0.1
+    keep = orc.keep_mask(123, 1, 4, S, p)
+    n = keep.size
+    rate = keep.mean()
+    assert abs(rate - (1 - p)) < 4 * math.sqrt(p * (1 - p) / n)
+    assert orc.keep_mask(0, 1, 1, 64, 0.0).all()
+    assert (keep[0, 0] != keep[0, 1]).mean() > 0.1            # heads differ
+    assert (keep != orc.keep_mask(124, 1, 4, S, p)).mean() > 0.1  # seeds differ
+    assert (keep[0, 0] != keep[0, 0].T).mean() > 0.1           # row/col not symmetric
+
+
+def test_seed_formula():
+    assert orc.next_seed(0, 1) == 1
+    assert orc.next_seed(1, 1) == (2654435761 + 1) & 0xFFFFFFFF
+    assert orc.next_seed(2 ** 40 + 3, 7) == ((2 ** 40 + 3) * 2654435761 + 7) % 2 ** 32
+
+
+def _rotate_half(x):
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat((-x2, x1), dim=-1)
+
+
+def test_rope_fwd_bitwise_vs_torch_eager():
+    S = 300
+    cos, sin = orc.rope_tables(S)
+    tc, ts = torch.from_numpy(cos), torch.from_numpy(sin)
+    x = torch.from_numpy(_rand((2, 3, S, 64), 8)).half()
+    ref = (x * tc + _rotate_half(x) * ts).half()
+    mine = orc.rope_fwd(x.numpy(), cos, sin)
+    assert np.array_equal(mine.view(np.uint16), ref.numpy().view(np.uint16))
+
+
+def test_rope_bwd_bitwise_vs_torch_autograd():
+    S = 300
+    cos, sin = orc.rope_tables(S)
+    tc, ts = torch.from_numpy(cos), torch.from_numpy(sin)
+    x = torch.from_numpy(_rand((2, 3, S, 64), 9)).float().requires_grad_(True)
+    g = torch.from_numpy(_rand((2, 3, S, 64), 10)).half()
+    out = x * tc + _rotate_half(x) * ts
+    out.backward(g.float())
+    ref = x.grad.half()
+    mine = orc.rope_bwd(g.numpy(), cos, sin)
+    assert np.array_equal(mine.view(np.uint16), ref.numpy().view(np.uint16))
+
+
+def test_rope_tables_match_train_py_construction():
+    """inv_freq over d_model 768 truncated to 64 columns: cos[:, d] != cos[:, d+32]."""
+    cos, sin = orc.rope_tables(64)
+    assert cos.shape == (64, 64)
+    assert not np.allclose(cos[:, :32], cos[:, 32:])
+    t = 5
+    assert abs(cos[t, 1] - math.cos(t * 10000 ** (-2 / 768))) < 1e-6
+
+
+def test_oracle_reproduces_golden_fixtures():
+    """The committed fixtures (SDPA-MATH fp64 for p=0, oracle for p>0) agree
+    with the oracle on the fp16 inputs they hold."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "fa2_golden.npz"))
+    names = sorted({k.split("/")[0] for k in z.files if not k.startswith("mask")})
+    assert len(names) >= 5
+    for name in names:
+        B, H, S, causal, scale, p, seed = z[f"{name}/meta"]
+        B, H, S, seed = int(B), int(H), int(S), int(seed)
+        q, k, v, do = (z[f"{name}/{t}"].astype(np.float64) for t in ("q", "k", "v", "do"))
+        keep = orc.keep_mask(seed, B, H, S, p) if p > 0 else None
+        if keep is not None:
+            assert np.array_equal(np.packbits(keep.reshape(-1)), z[f"{name}/keepbits"])
+        o, lse = orc.attention_tiled_fwd(q, k, v, causal=bool(causal), scale=scale, keep=keep, p=p)
+        dq, dk, dv, _ = orc.attention_bwd(q, k, v, o, lse, do, causal=bool(causal), scale=scale, keep=keep, p=p)
+        for mine, key in ((o, "o"), (lse, "lse"), (dq, "dq"), (dk, "dk"), (dv, "dv")):
+            assert orc.max_abs(mine, z[f"{name}/{key}"]) < 2e-5, (name, key)
+    for key in (k for k in z.files if k.startswith("mask/")):
+        _, seed, bh = key.split("/")
+        rows, cols = np.arange(64).reshape(64, 1), np.arange(64).reshape(1, 64)
+        assert np.array_equal(np.packbits(orc.dropout_keep(int(seed), rows, cols, int(bh), 0.1).reshape(-1)), z[key])

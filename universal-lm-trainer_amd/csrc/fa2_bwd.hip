@@ -1,0 +1,529 @@
+// fa2_bwd.hip -- causal FlashAttention-2 backward for gfx950 (MI355X).
+//
+// With S2 = scale*log2(e) * q.k and lse in natural log (the reference's
+// formulas, reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:10-25):
+//   P     = exp2(S2 - lse*log2(e))           (recomputed, never stored)
+//   P_d   = keep * P / (1-p)                 (same hash as the forward)
+//   delta = rowsum(O * dO)
+//   dS    = P_d * dP - P * delta,  dP = dO V^T
+//   dV    = P_d^T dO,  dK = scale * dS^T Q,  dQ = scale * dS K
+//
+// dQ accumulation: split pass, like the reference (its dQ and dK/dV kernels,
+// bwd.cu:66-428), with no atomics:
+//   * bwd_dq_kernel : a workgroup owns 256 queries, keeps Q^T, dO^T, lse and
+//     delta of its queries in registers and streams key tiles (K, V, K^T via
+//     LDS).  It also computes delta itself (the reference's pre-pass,
+//     bwd.cu:42-61) from the O and dO rows it holds and stores it for the
+//     dK/dV pass.  S^T and dP^T accumulators give each lane one query, so
+//     lse/delta are per-lane scalars and dS^T feeds the dQ^T = K^T dS^T MFMA
+//     straight from registers.
+//   * bwd_dkv_kernel: a workgroup owns 256 keys (64 per wave, K^T and V^T in
+//     registers), streams query tiles (Q, dO row-major and transposed, lse,
+//     delta via LDS) and accumulates dK^T and dV^T in registers; P and dS
+//     feed the dV/dK MFMAs straight from the S/dP accumulators.
+#include "fa2_device.h"
+#include "fa2_kernels.h"
+
+namespace fa2 {
+namespace {
+
+// ---------------------------------------------------------------------------
+// delta only (used when the caller asks for delta without dQ): 8 lanes/row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_delta_kernel(const BwdArgs a) {
+    const int S = a.S;
+    const int nrb = (S + 31) / 32;
+    const int bh = blockIdx.x / nrb;
+    const int row = (blockIdx.x - bh * nrb) * 32 + (threadIdx.x >> 3);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int part = threadIdx.x & 7;
+    float sum = 0.f;
+    if (row < S) {
+        const h8 ov = *reinterpret_cast<const h8 *>(a.o + b * a.osb + h * a.osh + row * a.oss + 8 * part);
+        const h8 dv = *reinterpret_cast<const h8 *>(a.dout + b * a.dosb + h * a.dosh + row * a.doss + 8 * part);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += (float)ov[e] * (float)dv[e];
+    }
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if (row < S && part == 0) a.delta[(int64_t)bh * S + row] = sum;
+}
+
+// ---------------------------------------------------------------------------
+// dQ pass (+ delta)
+// ---------------------------------------------------------------------------
+constexpr int DQ_NW = 4;
+constexpr int DQ_QB = 2;                    // 32-query blocks per wave
+constexpr int DQ_KT = 64;                   // keys per tile
+constexpr int DQ_QWG = DQ_NW * 32 * DQ_QB;  // 256 queries per workgroup
+
+template <bool CAUSAL, bool DROPOUT>
+__global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][DQ_KT * LDR];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][DQ_KT * LDR];
+    __shared__ __attribute__((aligned(16))) _Float16 sKt[2][HD * LDR];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
+    const int S = a.S;
+    const int BH = a.B * a.H;
+    const int nqblk = (S + DQ_QWG - 1) / DQ_QWG;
+    const int L = blockIdx.x;
+    const int qblk = nqblk - 1 - L / BH;
+    const int bh = L - (L / BH) * BH;
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    const _Float16 *Qp = a.q + b * a.qsb + h * a.qsh;
+    const _Float16 *Kp = a.k + b * a.ksb + h * a.ksh;
+    const _Float16 *Vp = a.v + b * a.vsb + h * a.vsh;
+    const _Float16 *Op = a.o + b * a.osb + h * a.osh;
+    const _Float16 *dOp = a.dout + b * a.dosb + h * a.dosh;
+    const float *Lp = a.lse + b * a.lsb + h * a.lsh;
+    _Float16 *dQp = a.dq + b * a.dqsb + h * a.dqsh;
+    float *Dp = a.delta + (int64_t)bh * S;
+
+    const int q_wg0 = qblk * DQ_QWG;
+    const int qw0 = q_wg0 + wave * 32 * DQ_QB;
+    const float scale2 = a.scale2;
+
+    // Resident per-query operands and row statistics.
+    h8 qf[DQ_QB][4], dof[DQ_QB][4];
+    float lse2[DQ_QB], dl[DQ_QB];
+#pragma unroll
+    for (int qb = 0; qb < DQ_QB; ++qb) {
+        const int q = qw0 + 32 * qb + c;
+        const bool valid = q < S;
+        float part = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            h8 qv = zero_h8(), dv = zero_h8(), ov = zero_h8();
+            if (valid) {
+                const int d0 = 16 * st + 8 * g2;
+                qv = *reinterpret_cast<const h8 *>(Qp + q * a.qss + d0);
+                dv = *reinterpret_cast<const h8 *>(dOp + q * a.doss + d0);
+                ov = *reinterpret_cast<const h8 *>(Op + q * a.oss + d0);
+            }
+            qf[qb][st] = a.negate ? neg_h8(qv) : qv;
+            dof[qb][st] = dv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)dv[e];
+        }
+        dl[qb] = part + xor32(part);
+        lse2[qb] = valid ? Lp[q] * LOG2E : INFINITY;
+        if (valid && g2 == 0) Dp[q] = dl[qb];
+    }
+
+    f16x dq[DQ_QB][2];
+#pragma unroll
+    for (int qb = 0; qb < DQ_QB; ++qb) {
+        dq[qb][0] = zero16();
+        dq[qb][1] = zero16();
+    }
+
+    const int kend = CAUSAL ? min(S, q_wg0 + DQ_QWG) : S;
+    const int ntiles = (kend + DQ_KT - 1) / DQ_KT;
+
+    const int lp = tid >> 3;
+    const int lc = (tid & 7) * 8;
+    h8 kr0, kr1, vr0, vr1;
+    auto gload = [&](int k0) {
+        const int r0 = k0 + 2 * lp, r1 = r0 + 1;
+        kr0 = zero_h8();
+        kr1 = zero_h8();
+        vr0 = zero_h8();
+        vr1 = zero_h8();
+        if (r0 < S) {
+            kr0 = *reinterpret_cast<const h8 *>(Kp + r0 * a.kss + lc);
+            vr0 = *reinterpret_cast<const h8 *>(Vp + r0 * a.vss + lc);
+        }
+        if (r1 < S) {
+            kr1 = *reinterpret_cast<const h8 *>(Kp + r1 * a.kss + lc);
+            vr1 = *reinterpret_cast<const h8 *>(Vp + r1 * a.vss + lc);
+        }
+    };
+    auto lstore = [&](int buf) {
+        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp) * LDR + lc]) = kr0;
+        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp + 1) * LDR + lc]) = kr1;
+        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp) * LDR + lc]) = vr0;
+        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp + 1) * LDR + lc]) = vr1;
+        const int pc = kperm(2 * lp);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h2 pr;
+            pr[0] = kr0[e];
+            pr[1] = kr1[e];
+            *reinterpret_cast<h2 *>(&sKt[buf][(lc + e) * LDR + pc]) = pr;
+        }
+    };
+
+    if (ntiles > 0) {
+        gload(0);
+        lstore(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        const int k0 = t * DQ_KT;
+        if (t + 1 < ntiles) gload(k0 + DQ_KT);
+
+        const bool active = (qw0 < S) && (!CAUSAL || k0 <= qw0 + 32 * DQ_QB - 1);
+        if (active) {
+            const _Float16 *tK = sK[buf];
+            const _Float16 *tV = sV[buf];
+            const _Float16 *tKt = sKt[buf];
+            const bool need_mask = (k0 + DQ_KT > S) || (CAUSAL && k0 + DQ_KT - 1 > qw0);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                // S^T = K Q^T and dP^T = V dO^T for 32 keys.
+                f16x s[DQ_QB], dp[DQ_QB];
+#pragma unroll
+                for (int qb = 0; qb < DQ_QB; ++qb) {
+                    s[qb] = zero16();
+                    dp[qb] = zero16();
+                }
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const h8 ka = *reinterpret_cast<const h8 *>(tK + (32 * kb + c) * LDR + 16 * st + 8 * g2);
+                    const h8 va = *reinterpret_cast<const h8 *>(tV + (32 * kb + c) * LDR + 16 * st + 8 * g2);
+#pragma unroll
+                    for (int qb = 0; qb < DQ_QB; ++qb) {
+                        s[qb] = mfma32(ka, qf[qb][st], s[qb]);
+                        dp[qb] = mfma32(va, dof[qb][st], dp[qb]);
+                    }
+                }
+                h8 dsb[DQ_QB][2];
+#pragma unroll
+                for (int qb = 0; qb < DQ_QB; ++qb) {
+                    const int q = qw0 + 32 * qb + c;
+                    if (need_mask) {
+                        const int lim = CAUSAL ? min(q, S - 1) : S - 1;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                            if (key > lim) s[qb][r] = -INFINITY;
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float p = __builtin_amdgcn_exp2f(fmaf(s[qb][r], scale2, -lse2[qb]));
+                        float g = dp[qb][r];
+                        if (DROPOUT) {
+                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                            g = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr) ? g * a.inv_keep : 0.f;
+                        }
+                        s[qb][r] = p * (g - dl[qb]);
+                    }
+                    dsb[qb][0] = acc_to_h8(s[qb], 0);
+                    dsb[qb][1] = acc_to_h8(s[qb], 1);
+                }
+                // dQ^T += K^T dS^T over these 32 keys.
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const h8 ka = *reinterpret_cast<const h8 *>(
+                            tKt + (32 * db + c) * LDR + 32 * kb + 16 * hh + 8 * g2);
+#pragma unroll
+                        for (int qb = 0; qb < DQ_QB; ++qb) dq[qb][db] = mfma32(ka, dsb[qb][hh], dq[qb][db]);
+                    }
+            }
+        }
+
+        if (t + 1 < ntiles) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float sc = a.scale;
+#pragma unroll
+    for (int qb = 0; qb < DQ_QB; ++qb) {
+        const int q = qw0 + 32 * qb + c;
+        if (q < S) {
+            _Float16 *row = dQp + q * a.dqss;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f4 x;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[j] = dq[qb][db][4 * i + j] * sc;
+                    *reinterpret_cast<h4 *>(row + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(x, h4);
+                }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV pass
+// ---------------------------------------------------------------------------
+constexpr int KV_NW = 4;
+constexpr int KV_KB = 2;                    // 32-key blocks per wave
+constexpr int KV_QT = 64;                   // queries per tile
+constexpr int KV_KWG = KV_NW * 32 * KV_KB;  // 256 keys per workgroup
+
+template <bool CAUSAL, bool DROPOUT>
+__global__ __launch_bounds__(256) void bwd_dkv_kernel(const BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 sQ[2][KV_QT * LDR];
+    __shared__ __attribute__((aligned(16))) _Float16 sdO[2][KV_QT * LDR];
+    __shared__ __attribute__((aligned(16))) _Float16 sQt[2][HD * LDR];
+    __shared__ __attribute__((aligned(16))) _Float16 sdOt[2][HD * LDR];
+    __shared__ __attribute__((aligned(16))) float sL[2][KV_QT];
+    __shared__ __attribute__((aligned(16))) float sD[2][KV_QT];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
+    const int S = a.S;
+    const int BH = a.B * a.H;
+    const int L = blockIdx.x;
+    const int kblk = L / BH;
+    const int bh = L - kblk * BH;
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    const _Float16 *Qp = a.q + b * a.qsb + h * a.qsh;
+    const _Float16 *Kp = a.k + b * a.ksb + h * a.ksh;
+    const _Float16 *Vp = a.v + b * a.vsb + h * a.vsh;
+    const _Float16 *dOp = a.dout + b * a.dosb + h * a.dosh;
+    const float *Lp = a.lse + b * a.lsb + h * a.lsh;
+    const float *Dp = a.delta + (int64_t)bh * S;
+    _Float16 *dKp = a.dk + b * a.dksb + h * a.dksh;
+    _Float16 *dVp = a.dv + b * a.dvsb + h * a.dvsh;
+
+    const int k_wg0 = kblk * KV_KWG;
+    const int kw0 = k_wg0 + wave * 32 * KV_KB;
+    const float scale2 = a.scale2;
+
+    // Resident K^T / V^T B operands: lane holds key (kw0 + 32*kb + c).
+    h8 kf[KV_KB][4], vf[KV_KB][4];
+#pragma unroll
+    for (int kb = 0; kb < KV_KB; ++kb) {
+        const int key = kw0 + 32 * kb + c;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            h8 kv = zero_h8(), vv = zero_h8();
+            if (key < S) {
+                kv = *reinterpret_cast<const h8 *>(Kp + key * a.kss + 16 * st + 8 * g2);
+                vv = *reinterpret_cast<const h8 *>(Vp + key * a.vss + 16 * st + 8 * g2);
+            }
+            kf[kb][st] = a.negate ? neg_h8(kv) : kv;
+            vf[kb][st] = vv;
+        }
+    }
+
+    f16x dk[KV_KB][2], dv[KV_KB][2];
+#pragma unroll
+    for (int kb = 0; kb < KV_KB; ++kb) {
+        dk[kb][0] = zero16();
+        dk[kb][1] = zero16();
+        dv[kb][0] = zero16();
+        dv[kb][1] = zero16();
+    }
+
+    const int q_start = CAUSAL ? (k_wg0 / KV_QT) * KV_QT : 0;
+    const int ntiles = (k_wg0 < S) ? (S - q_start + KV_QT - 1) / KV_QT : 0;
+
+    const int lp = tid >> 3;
+    const int lc = (tid & 7) * 8;
+    h8 qr0, qr1, dr0, dr1;
+    float lr = 0.f, drr = 0.f;
+    auto gload = [&](int q0) {
+        const int r0 = q0 + 2 * lp, r1 = r0 + 1;
+        qr0 = zero_h8();
+        qr1 = zero_h8();
+        dr0 = zero_h8();
+        dr1 = zero_h8();
+        if (r0 < S) {
+            qr0 = *reinterpret_cast<const h8 *>(Qp + r0 * a.qss + lc);
+            dr0 = *reinterpret_cast<const h8 *>(dOp + r0 * a.doss + lc);
+        }
+        if (r1 < S) {
+            qr1 = *reinterpret_cast<const h8 *>(Qp + r1 * a.qss + lc);
+            dr1 = *reinterpret_cast<const h8 *>(dOp + r1 * a.doss + lc);
+        }
+        if (tid < KV_QT) {
+            const int q = q0 + tid;
+            lr = q < S ? Lp[q] * LOG2E : INFINITY;
+            drr = q < S ? Dp[q] : 0.f;
+        }
+    };
+    auto lstore = [&](int buf) {
+        *reinterpret_cast<h8 *>(&sQ[buf][(2 * lp) * LDR + lc]) = qr0;
+        *reinterpret_cast<h8 *>(&sQ[buf][(2 * lp + 1) * LDR + lc]) = qr1;
+        *reinterpret_cast<h8 *>(&sdO[buf][(2 * lp) * LDR + lc]) = dr0;
+        *reinterpret_cast<h8 *>(&sdO[buf][(2 * lp + 1) * LDR + lc]) = dr1;
+        const int pc = kperm(2 * lp);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h2 pq, pd;
+            pq[0] = qr0[e];
+            pq[1] = qr1[e];
+            pd[0] = dr0[e];
+            pd[1] = dr1[e];
+            *reinterpret_cast<h2 *>(&sQt[buf][(lc + e) * LDR + pc]) = pq;
+            *reinterpret_cast<h2 *>(&sdOt[buf][(lc + e) * LDR + pc]) = pd;
+        }
+        if (tid < KV_QT) {
+            sL[buf][tid] = lr;
+            sD[buf][tid] = drr;
+        }
+    };
+
+    if (ntiles > 0) {
+        gload(q_start);
+        lstore(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        const int q0 = q_start + t * KV_QT;
+        if (t + 1 < ntiles) gload(q0 + KV_QT);
+
+        const bool active = (kw0 < S) && (!CAUSAL || q0 + KV_QT - 1 >= kw0);
+        if (active) {
+            const _Float16 *tQ = sQ[buf];
+            const _Float16 *tdO = sdO[buf];
+            const _Float16 *tQt = sQt[buf];
+            const _Float16 *tdOt = sdOt[buf];
+#pragma unroll
+            for (int qb = 0; qb < KV_QT / 32; ++qb) {
+                if (CAUSAL && q0 + 32 * qb + 31 < kw0) continue;  // whole block above the diagonal
+                // S = Q K^T and dP = dO V^T : rows = queries, cols = this lane's key.
+                f16x s[KV_KB], dp[KV_KB];
+#pragma unroll
+                for (int kb = 0; kb < KV_KB; ++kb) {
+                    s[kb] = zero16();
+                    dp[kb] = zero16();
+                }
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const h8 qa = *reinterpret_cast<const h8 *>(tQ + (32 * qb + c) * LDR + 16 * st + 8 * g2);
+                    const h8 da = *reinterpret_cast<const h8 *>(tdO + (32 * qb + c) * LDR + 16 * st + 8 * g2);
+#pragma unroll
+                    for (int kb = 0; kb < KV_KB; ++kb) {
+                        s[kb] = mfma32(qa, kf[kb][st], s[kb]);
+                        dp[kb] = mfma32(da, vf[kb][st], dp[kb]);
+                    }
+                }
+                f4 l4[4], d4[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    l4[i] = *reinterpret_cast<const f4 *>(&sL[buf][32 * qb + 8 * i + 4 * g2]);
+                    d4[i] = *reinterpret_cast<const f4 *>(&sD[buf][32 * qb + 8 * i + 4 * g2]);
+                }
+                const bool need_mask = CAUSAL && (q0 + 32 * qb < kw0 + 32 * KV_KB - 1);
+                h8 pb[KV_KB][2], dsb[KV_KB][2];
+#pragma unroll
+                for (int kb = 0; kb < KV_KB; ++kb) {
+                    const int key = kw0 + 32 * kb + c;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int q = q0 + 32 * qb + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                        float sv = s[kb][r];
+                        if (need_mask && key > q) sv = -INFINITY;
+                        const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -l4[r >> 2][r & 3]));
+                        const float del = d4[r >> 2][r & 3];
+                        float pd = p, ds;
+                        if (DROPOUT) {
+                            const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
+                            pd = keep ? p * a.inv_keep : 0.f;
+                            ds = pd * dp[kb][r] - p * del;
+                        } else {
+                            ds = p * (dp[kb][r] - del);
+                        }
+                        s[kb][r] = pd;
+                        dp[kb][r] = ds;
+                    }
+                    pb[kb][0] = acc_to_h8(s[kb], 0);
+                    pb[kb][1] = acc_to_h8(s[kb], 1);
+                    dsb[kb][0] = acc_to_h8(dp[kb], 0);
+                    dsb[kb][1] = acc_to_h8(dp[kb], 1);
+                }
+                // dV^T += dO^T P and dK^T += Q^T dS, contracting 16 queries per step.
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int off = (32 * db + c) * LDR + 32 * qb + 16 * hh + 8 * g2;
+                        const h8 da = *reinterpret_cast<const h8 *>(tdOt + off);
+                        const h8 qa = *reinterpret_cast<const h8 *>(tQt + off);
+#pragma unroll
+                        for (int kb = 0; kb < KV_KB; ++kb) {
+                            dv[kb][db] = mfma32(da, pb[kb][hh], dv[kb][db]);
+                            dk[kb][db] = mfma32(qa, dsb[kb][hh], dk[kb][db]);
+                        }
+                    }
+            }
+        }
+
+        if (t + 1 < ntiles) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float sc = a.scale;
+#pragma unroll
+    for (int kb = 0; kb < KV_KB; ++kb) {
+        const int key = kw0 + 32 * kb + c;
+        if (key < S) {
+            _Float16 *krow = dKp + key * a.dkss;
+            _Float16 *vrow = dVp + key * a.dvss;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f4 xk, xv;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        xk[j] = dk[kb][db][4 * i + j] * sc;
+                        xv[j] = dv[kb][db][4 * i + j];
+                    }
+                    *reinterpret_cast<h4 *>(krow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xk, h4);
+                    *reinterpret_cast<h4 *>(vrow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xv, h4);
+                }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st) {
+    const int nrb = (a.S + 31) / 32;
+    hipLaunchKernelGGL(bwd_delta_kernel, dim3((unsigned)(nrb * a.B * a.H)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    const int nqblk = (a.S + DQ_QWG - 1) / DQ_QWG;
+    const dim3 grid((unsigned)(nqblk * a.B * a.H)), block(256);
+    if (causal) {
+        if (dropout)
+            hipLaunchKernelGGL((bwd_dq_kernel<true, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((bwd_dq_kernel<true, false>), grid, block, 0, st, a);
+    } else {
+        if (dropout)
+            hipLaunchKernelGGL((bwd_dq_kernel<false, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((bwd_dq_kernel<false, false>), grid, block, 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    const int nkblk = (a.S + KV_KWG - 1) / KV_KWG;
+    const dim3 grid((unsigned)(nkblk * a.B * a.H)), block(256);
+    if (causal) {
+        if (dropout)
+            hipLaunchKernelGGL((bwd_dkv_kernel<true, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((bwd_dkv_kernel<true, false>), grid, block, 0, st, a);
+    } else {
+        if (dropout)
+            hipLaunchKernelGGL((bwd_dkv_kernel<false, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((bwd_dkv_kernel<false, false>), grid, block, 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fa2

@@ -1,0 +1,249 @@
+// fa2_capi.hip -- the C ABI (include/fa2_mi355x.h): argument validation,
+// kernel-argument packing and launches.  Allocates nothing, keeps no state
+// besides a thread-local error message, never synchronises.
+#include <float.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/fa2_mi355x.h"
+#include "fa2_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = {0};
+
+int fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Largest element offset reachable by a [B,H,S,64] view with these strides
+// must fit int64 and each stride must keep 16-byte row alignment.
+int check_tensor(const char *name, const void *ptr, const int64_t st[3], int32_t B, int32_t H, int32_t S,
+                 bool vec16) {
+    if (!ptr) return fail(FA2_ERR_NULL_POINTER, "%s is NULL", name);
+    for (int i = 0; i < 3; ++i) {
+        if (st[i] < 0) return fail(FA2_ERR_BAD_SHAPE, "%s stride[%d] = %lld is negative", name, i, (long long)st[i]);
+        if (vec16 && (st[i] % 8) != 0)
+            return fail(FA2_ERR_MISALIGNED, "%s stride[%d] = %lld is not a multiple of 8 elements", name, i,
+                        (long long)st[i]);
+        if (!vec16 && (st[i] % 2) != 0)
+            return fail(FA2_ERR_MISALIGNED, "%s stride[%d] = %lld is odd", name, i, (long long)st[i]);
+    }
+    if (vec16 && !aligned16(ptr)) return fail(FA2_ERR_MISALIGNED, "%s is not 16-byte aligned", name);
+    if (!vec16 && (reinterpret_cast<uintptr_t>(ptr) & 3u))
+        return fail(FA2_ERR_MISALIGNED, "%s is not 4-byte aligned", name);
+    const double span = (double)(B - 1) * st[0] + (double)(H - 1) * st[1] + (double)(S - 1) * st[2] + 64.0;
+    if (span > 9.0e18) return fail(FA2_ERR_BAD_SHAPE, "%s spans more than 2^63 elements", name);
+    return FA2_OK;
+}
+
+int check_shape(int32_t B, int32_t H, int32_t S, int32_t D, int per_wg) {
+    if (B < 0 || H < 0 || S < 0) return fail(FA2_ERR_BAD_SHAPE, "negative size B=%d H=%d S=%d", B, H, S);
+    if (D != FA2_HEAD_DIM) return fail(FA2_ERR_BAD_SHAPE, "head dim %d unsupported (must be 64)", D);
+    const double grid = (double)B * H * ((S + per_wg - 1) / per_wg + 1);
+    if (grid > 2147483647.0 || (double)B * H * S > 2147483647.0)
+        return fail(FA2_ERR_BAD_SHAPE, "B*H*S = %.0f exceeds the int32 grid limit", (double)B * H * S);
+    return FA2_OK;
+}
+
+int check_scale_dropout(float scale, float p) {
+    if (!isfinite(scale)) return fail(FA2_ERR_BAD_ARGUMENT, "softmax_scale %g is not finite", (double)scale);
+    if (!(p >= 0.f && p < 1.f)) return fail(FA2_ERR_BAD_ARGUMENT, "dropout_p %g outside [0, 1)", (double)p);
+    return FA2_OK;
+}
+
+float scale2_of(float scale) {
+    const float s2 = fabsf(scale) * 1.4426950408889634f;  // log2(e)
+    return s2 < FLT_MIN ? FLT_MIN : s2;
+}
+
+// keep iff (hash >> 8) * 2^-24 >= p  <=>  (hash >> 8) >= ceil(p * 2^24)
+uint32_t drop_threshold(float p) { return (uint32_t)ceilf(p * 16777216.0f); }
+
+}  // namespace
+
+extern "C" {
+
+const char *fa2_status_string(int status) {
+    switch (status) {
+        case FA2_OK: return "ok";
+        case FA2_ERR_NULL_POINTER: return "null pointer";
+        case FA2_ERR_BAD_SHAPE: return "bad shape";
+        case FA2_ERR_MISALIGNED: return "misaligned pointer or stride";
+        case FA2_ERR_BAD_ARGUMENT: return "bad argument";
+        case FA2_ERR_WORKSPACE: return "workspace missing or too small";
+        case FA2_ERR_LAUNCH: return "kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+const char *fa2_last_error(void) { return g_err; }
+
+const char *fa2_version(void) { return "fa2_mi355x 0.1 (gfx950, fp16 MFMA 32x32x16)"; }
+
+int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
+    g_err[0] = 0;
+    if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
+    int rc = check_shape(p->B, p->H, p->S, p->D, 256);
+    if (rc) return rc;
+    if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
+    if ((int64_t)p->B * p->H * p->S == 0) return FA2_OK;
+    if ((rc = check_tensor("q", p->q, p->q_stride, p->B, p->H, p->S, true))) return rc;
+    if ((rc = check_tensor("k", p->k, p->k_stride, p->B, p->H, p->S, true))) return rc;
+    if ((rc = check_tensor("v", p->v, p->v_stride, p->B, p->H, p->S, true))) return rc;
+    if ((rc = check_tensor("o", p->o, p->o_stride, p->B, p->H, p->S, false))) return rc;
+    if (!aligned16(p->o) || (p->o_stride[0] | p->o_stride[1] | p->o_stride[2]) % 4)
+        return fail(FA2_ERR_MISALIGNED, "o needs 16-byte base alignment and strides that are multiples of 4");
+    if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
+    if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
+    if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
+
+    fa2::FwdArgs a;
+    a.q = static_cast<const _Float16 *>(p->q);
+    a.k = static_cast<const _Float16 *>(p->k);
+    a.v = static_cast<const _Float16 *>(p->v);
+    a.o = static_cast<_Float16 *>(p->o);
+    a.lse = p->lse;
+    a.qsb = p->q_stride[0]; a.qsh = p->q_stride[1]; a.qss = p->q_stride[2];
+    a.ksb = p->k_stride[0]; a.ksh = p->k_stride[1]; a.kss = p->k_stride[2];
+    a.vsb = p->v_stride[0]; a.vsh = p->v_stride[1]; a.vss = p->v_stride[2];
+    a.osb = p->o_stride[0]; a.osh = p->o_stride[1]; a.oss = p->o_stride[2];
+    a.lsb = p->lse_stride[0]; a.lsh = p->lse_stride[1];
+    a.B = p->B; a.H = p->H; a.S = p->S;
+    a.scale2 = scale2_of(p->softmax_scale);
+    a.negate = p->softmax_scale < 0.f;
+    a.seed = p->seed;
+    a.drop_thr = drop_threshold(p->dropout_p);
+    a.inv_keep = 1.f / (1.f - p->dropout_p);
+    const hipError_t e = fa2::launch_fwd(a, p->causal != 0, p->dropout_p > 0.f, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "forward launch: %s", hipGetErrorString(e));
+    return FA2_OK;
+}
+
+size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S) {
+    if (B <= 0 || H <= 0 || S <= 0) return 0;
+    return (size_t)B * H * S * sizeof(float);
+}
+
+int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
+    if (mode < 0 || mode > 7) return fail(FA2_ERR_BAD_ARGUMENT, "mode %d outside 0..7", mode);
+    int rc = check_shape(p->B, p->H, p->S, p->D, 256);
+    if (rc) return rc;
+    if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
+    if ((int64_t)p->B * p->H * p->S == 0 || mode == 0) return FA2_OK;
+    const size_t need = fa2_bwd_workspace_bytes(p->B, p->H, p->S);
+    if (!workspace || workspace_bytes < need)
+        return fail(FA2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : 0);
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u)
+        return fail(FA2_ERR_MISALIGNED, "workspace is not 16-byte aligned");
+    const bool want_delta = mode & 1, want_dq = mode & 2, want_dkv = mode & 4;
+    if ((rc = check_tensor("o", p->o, p->o_stride, p->B, p->H, p->S, true))) return rc;
+    if ((rc = check_tensor("dout", p->dout, p->do_stride, p->B, p->H, p->S, true))) return rc;
+    if (want_dq || want_dkv) {
+        if ((rc = check_tensor("q", p->q, p->q_stride, p->B, p->H, p->S, true))) return rc;
+        if ((rc = check_tensor("k", p->k, p->k_stride, p->B, p->H, p->S, true))) return rc;
+        if ((rc = check_tensor("v", p->v, p->v_stride, p->B, p->H, p->S, true))) return rc;
+        if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
+        if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
+        if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
+    }
+    struct Out { const char *name; void *ptr; const int64_t *st; };
+    const Out outs[3] = {{"dq", p->dq, p->dq_stride}, {"dk", p->dk, p->dk_stride}, {"dv", p->dv, p->dv_stride}};
+    for (int i = 0; i < 3; ++i) {
+        if (i == 0 && !want_dq) continue;
+        if (i > 0 && !want_dkv) continue;
+        if ((rc = check_tensor(outs[i].name, outs[i].ptr, outs[i].st, p->B, p->H, p->S, false))) return rc;
+        if (!aligned16(outs[i].ptr) || (outs[i].st[0] | outs[i].st[1] | outs[i].st[2]) % 4)
+            return fail(FA2_ERR_MISALIGNED, "%s needs 16-byte base alignment and strides that are multiples of 4",
+                        outs[i].name);
+    }
+
+    fa2::BwdArgs a;
+    a.q = static_cast<const _Float16 *>(p->q);
+    a.k = static_cast<const _Float16 *>(p->k);
+    a.v = static_cast<const _Float16 *>(p->v);
+    a.o = static_cast<const _Float16 *>(p->o);
+    a.dout = static_cast<const _Float16 *>(p->dout);
+    a.lse = p->lse;
+    a.dq = static_cast<_Float16 *>(p->dq);
+    a.dk = static_cast<_Float16 *>(p->dk);
+    a.dv = static_cast<_Float16 *>(p->dv);
+    a.delta = static_cast<float *>(workspace);
+    a.qsb = p->q_stride[0]; a.qsh = p->q_stride[1]; a.qss = p->q_stride[2];
+    a.ksb = p->k_stride[0]; a.ksh = p->k_stride[1]; a.kss = p->k_stride[2];
+    a.vsb = p->v_stride[0]; a.vsh = p->v_stride[1]; a.vss = p->v_stride[2];
+    a.osb = p->o_stride[0]; a.osh = p->o_stride[1]; a.oss = p->o_stride[2];
+    a.dosb = p->do_stride[0]; a.dosh = p->do_stride[1]; a.doss = p->do_stride[2];
+    a.dqsb = p->dq_stride[0]; a.dqsh = p->dq_stride[1]; a.dqss = p->dq_stride[2];
+    a.dksb = p->dk_stride[0]; a.dksh = p->dk_stride[1]; a.dkss = p->dk_stride[2];
+    a.dvsb = p->dv_stride[0]; a.dvsh = p->dv_stride[1]; a.dvss = p->dv_stride[2];
+    a.lsb = p->lse_stride[0]; a.lsh = p->lse_stride[1];
+    a.B = p->B; a.H = p->H; a.S = p->S;
+    a.scale = p->softmax_scale;
+    a.scale2 = scale2_of(p->softmax_scale);
+    a.negate = p->softmax_scale < 0.f;
+    a.seed = p->seed;
+    a.drop_thr = drop_threshold(p->dropout_p);
+    a.inv_keep = 1.f / (1.f - p->dropout_p);
+    const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
+    const hipStream_t st = (hipStream_t)stream;
+
+    hipError_t e = hipSuccess;
+    if (want_dq) {
+        e = fa2::launch_bwd_dq(a, causal, dropout, st);  // also writes delta
+        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "dQ launch: %s", hipGetErrorString(e));
+    } else if (want_delta) {
+        e = fa2::launch_bwd_delta(a, st);
+        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "delta launch: %s", hipGetErrorString(e));
+    }
+    if (want_dkv) {
+        e = fa2::launch_bwd_dkv(a, causal, dropout, st);
+        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "dK/dV launch: %s", hipGetErrorString(e));
+    }
+    return FA2_OK;
+}
+
+int fa2_rope_f16(const fa2_rope_params *p, int32_t backward, void *stream) {
+    g_err[0] = 0;
+    if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
+    int rc = check_shape(p->B, p->H, p->S, p->D, 8);
+    if (rc) return rc;
+    if ((int64_t)p->B * p->H * p->S == 0) return FA2_OK;
+    if ((rc = check_tensor("q", p->q, p->q_stride, p->B, p->H, p->S, false))) return rc;
+    if ((rc = check_tensor("k", p->k, p->k_stride, p->B, p->H, p->S, false))) return rc;
+    if ((rc = check_tensor("qo", p->qo, p->qo_stride, p->B, p->H, p->S, false))) return rc;
+    if ((rc = check_tensor("ko", p->ko, p->ko_stride, p->B, p->H, p->S, false))) return rc;
+    if (!p->cos || !p->sin) return fail(FA2_ERR_NULL_POINTER, "cos/sin is NULL");
+    if ((reinterpret_cast<uintptr_t>(p->cos) | reinterpret_cast<uintptr_t>(p->sin)) & 3u)
+        return fail(FA2_ERR_MISALIGNED, "cos/sin are not 4-byte aligned");
+    if (p->cs_stride < 0 || p->sn_stride < 0) return fail(FA2_ERR_BAD_SHAPE, "negative cos/sin stride");
+    fa2::RopeArgs a;
+    a.q = static_cast<const _Float16 *>(p->q);
+    a.k = static_cast<const _Float16 *>(p->k);
+    a.qo = static_cast<_Float16 *>(p->qo);
+    a.ko = static_cast<_Float16 *>(p->ko);
+    a.cs = p->cos;
+    a.sn = p->sin;
+    a.qsb = p->q_stride[0]; a.qsh = p->q_stride[1]; a.qss = p->q_stride[2];
+    a.ksb = p->k_stride[0]; a.ksh = p->k_stride[1]; a.kss = p->k_stride[2];
+    a.oqb = p->qo_stride[0]; a.oqh = p->qo_stride[1]; a.oqs = p->qo_stride[2];
+    a.okb = p->ko_stride[0]; a.okh = p->ko_stride[1]; a.oks = p->ko_stride[2];
+    a.cs0 = p->cs_stride;
+    a.sn0 = p->sn_stride;
+    a.B = p->B; a.H = p->H; a.S = p->S;
+    const hipError_t e = fa2::launch_rope(a, backward != 0, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "rope launch: %s", hipGetErrorString(e));
+    return FA2_OK;
+}
+
+}  // extern "C"

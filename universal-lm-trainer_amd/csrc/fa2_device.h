@@ -1,0 +1,98 @@
+// fa2_device.h -- device-side building blocks shared by the gfx950 attention
+// kernels: vector types, the fp16 MFMA wrapper, the LDS row swizzle, the
+// dropout hash and small cross-lane helpers.
+//
+// Register layouts of v_mfma_f32_32x32x16_f16 (wave64, lane = 32*g2 + c):
+//   A operand (32 x 16, half8): lane holds A[m = c][k = 8*g2 + e], e = 0..7
+//   B operand (16 x 32, half8): lane holds B[k = 8*g2 + e][n = c]
+//   C/D       (32 x 32, 16 f32): register r = 4*i + j holds
+//             D[m = 8*i + 4*g2 + j][n = c]
+// The product only needs A and B to agree on which logical k sits in
+// (g2, e), so the kernels feed a logical k order of their own choosing into
+// both operands.  The one they use lets an accumulator be reused as the B
+// operand of the next MFMA without leaving registers: registers 8*hh .. 8*hh+7
+// of an accumulator hold rows 16*hh + 8*(e/4) + 4*g2 + (e%4), which is exactly
+// the k order of a 16-deep B operand.  The A operand read from LDS must then
+// present its k index in that order, which the LDS layouts below provide by
+// swapping bits 2 and 3 of the k index within each 16-group (kperm).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa2 {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f8 __attribute__((ext_vector_type(8)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+
+constexpr int HD = 64;        // head dimension (the only one supported)
+constexpr int LDR = HD + 8;   // LDS row stride in halves: 144 B keeps 16-byte
+                              // reads by 16 lanes on distinct banks
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f16x zero16() {
+    f16x z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    return z;
+}
+
+__device__ __forceinline__ h8 zero_h8() {
+    h8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (_Float16)0.f;
+    return z;
+}
+
+// Position of logical index k inside its LDS row: bits 2 and 3 swapped, so
+// that the 8 k values one lane feeds to a 16-deep MFMA step are contiguous.
+__device__ __forceinline__ int kperm(int k) {
+    return (k & ~0xC) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+// Registers 8*hh .. 8*hh+7 of an accumulator, rounded to fp16 (RNE): the B
+// operand of the next 16-deep MFMA step.
+__device__ __forceinline__ h8 acc_to_h8(const f16x &acc, int hh) {
+    f8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = acc[8 * hh + e];
+    return __builtin_convertvector(x, h8);
+}
+
+// Flip the sign of all eight halves (exact); used to fold a negative softmax
+// scale into one operand.
+__device__ __forceinline__ h8 neg_h8(h8 v) { return -v; }
+
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+// Dropout keep decision for element (row = query, col = key) of head bh.
+// The integer function is the reference's (reference @ None:
+// csrc/flash_attn_v100/fa_common.cuh:21-38): the "lowbias32" finaliser over
+// seed*0x9E3779B1 ^ (row+1)*0x85EBCA6B ^ (col+1)*0xC2B2AE35 ^ (bh+1)*0x27D4EB2F,
+// keep iff (h >> 8) * 2^-24 >= p.  Since (h >> 8) < 2^24 that fp32 compare is
+// exact and equals (h >> 8) >= thr with thr = ceil(p * 2^24), computed on the
+// host, so the kernels stay in integer arithmetic.
+__device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, uint32_t bh,
+                                             uint32_t thr) {
+    uint32_t x = seed * 0x9E3779B1u;
+    x ^= (uint32_t)(row + 1) * 0x85EBCA6Bu;
+    x ^= (uint32_t)(col + 1) * 0xC2B2AE35u;
+    x ^= (bh + 1u) * 0x27D4EB2Fu;
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return (x >> 8) >= thr;
+}
+
+}  // namespace fa2

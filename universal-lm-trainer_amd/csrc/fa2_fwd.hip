@@ -1,0 +1,285 @@
+// fa2_fwd.hip -- causal FlashAttention-2 forward for gfx950 (MI355X).
+//
+// Computes, per (b, h) and query row i,
+//   O[i]   = sum_j softmax_j(scale * q_i . k_j, j visible) * keep_ij/(1-p) * v_j
+//   LSE[i] = ln sum_{j visible} exp(scale * q_i . k_j)
+// following the reference's algorithm and guards (reference @ None:
+// csrc/flash_attn_v100/flash_attn_v100.cu:109-308): online softmax over key
+// tiles, causal tiles past the diagonal skipped, the denominator summed from
+// the un-dropped P, O = acc / l with l == 0 -> 0, LSE in natural log.
+//
+// Work decomposition (one workgroup = 4 waves = 256 queries of one (b, h)):
+//   * each wave owns 64 queries as two 32-query blocks; their Q^T operands
+//     (16 x 32 fp16 per d-step) stay in registers for the whole kernel;
+//   * key tiles of 64 are staged through LDS, double buffered: K row-major
+//     (A operand of S^T = K Q^T) and V transposed with the kperm swizzle
+//     (A operand of O^T = V^T P^T); the next tile's global loads are in
+//     flight while the current tile is computed, one barrier per tile;
+//   * S^T accumulators give each lane one query and 32 keys, so the row max
+//     is a local max plus one cross-half exchange, the running sum l stays a
+//     per-lane partial until the epilogue, the O^T rescale is a per-lane
+//     scalar, and P goes from the accumulator straight into the B operand of
+//     the PV MFMA (no LDS round trip);
+//   * workgroups are issued heaviest first (last query blocks first) and all
+//     workgroups of one (b, h) share blockIdx % 8, i.e. one XCD and its L2.
+#include "fa2_device.h"
+#include "fa2_kernels.h"
+
+namespace fa2 {
+namespace {
+
+constexpr int NW = 4;              // waves per workgroup
+constexpr int QB = 2;              // 32-query blocks per wave
+constexpr int KT = 64;             // keys per tile
+constexpr int QWG = NW * 32 * QB;  // queries per workgroup
+
+template <bool CAUSAL, bool DROPOUT>
+__global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][KT * LDR];
+    __shared__ __attribute__((aligned(16))) _Float16 sVt[2][HD * LDR];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
+    const int S = a.S;
+    const int BH = a.B * a.H;
+    const int nqblk = (S + QWG - 1) / QWG;
+    const int L = blockIdx.x;
+    const int qblk = nqblk - 1 - L / BH;
+    const int bh = L - (L / BH) * BH;
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    const _Float16 *Qp = a.q + b * a.qsb + h * a.qsh;
+    const _Float16 *Kp = a.k + b * a.ksb + h * a.ksh;
+    const _Float16 *Vp = a.v + b * a.vsb + h * a.vsh;
+    _Float16 *Op = a.o + b * a.osb + h * a.osh;
+    float *Lp = a.lse + b * a.lsb + h * a.lsh;
+
+    const int q_wg0 = qblk * QWG;
+    const int qw0 = q_wg0 + wave * 32 * QB;
+    const float scale2 = a.scale2;
+
+    // Q^T operands: lane holds query (qw0 + 32*qb + c), d = 16*st + 8*g2 + e.
+    h8 qf[QB][4];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int q = qw0 + 32 * qb + c;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            h8 v = zero_h8();
+            if (q < S) v = *reinterpret_cast<const h8 *>(Qp + q * a.qss + 16 * st + 8 * g2);
+            qf[qb][st] = a.negate ? neg_h8(v) : v;
+        }
+    }
+
+    f16x o[QB][2];
+    float m[QB], l[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        o[qb][0] = zero16();
+        o[qb][1] = zero16();
+        m[qb] = -INFINITY;
+        l[qb] = 0.f;
+    }
+
+    const int kend = CAUSAL ? min(S, q_wg0 + QWG) : S;
+    const int ntiles = (kend + KT - 1) / KT;
+
+    // Cooperative tile loader: thread -> key pair (2*lp, 2*lp+1), d chunk lc.
+    const int lp = tid >> 3;
+    const int lc = (tid & 7) * 8;
+    h8 kr0, kr1, vr0, vr1;
+    auto gload = [&](int k0) {
+        const int r0 = k0 + 2 * lp, r1 = r0 + 1;
+        kr0 = zero_h8();
+        kr1 = zero_h8();
+        vr0 = zero_h8();
+        vr1 = zero_h8();
+        if (r0 < S) {
+            kr0 = *reinterpret_cast<const h8 *>(Kp + r0 * a.kss + lc);
+            vr0 = *reinterpret_cast<const h8 *>(Vp + r0 * a.vss + lc);
+        }
+        if (r1 < S) {
+            kr1 = *reinterpret_cast<const h8 *>(Kp + r1 * a.kss + lc);
+            vr1 = *reinterpret_cast<const h8 *>(Vp + r1 * a.vss + lc);
+        }
+    };
+    auto lstore = [&](int buf) {
+        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp) * LDR + lc]) = kr0;
+        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp + 1) * LDR + lc]) = kr1;
+        const int pc = kperm(2 * lp);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h2 pr;
+            pr[0] = vr0[e];
+            pr[1] = vr1[e];
+            *reinterpret_cast<h2 *>(&sVt[buf][(lc + e) * LDR + pc]) = pr;
+        }
+    };
+
+    if (ntiles > 0) {
+        gload(0);
+        lstore(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        const int k0 = t * KT;
+        if (t + 1 < ntiles) gload(k0 + KT);
+
+        const bool active = (qw0 < S) && (!CAUSAL || k0 <= qw0 + 32 * QB - 1);
+        if (active) {
+            const _Float16 *tK = sK[buf];
+            const _Float16 *tVt = sVt[buf];
+
+            // S^T = K Q^T : s[qb][kb] rows = keys k0 + 32*kb + (8i+4g2+j), col = query.
+            f16x s[QB][2];
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                s[qb][0] = zero16();
+                s[qb][1] = zero16();
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const h8 ka0 = *reinterpret_cast<const h8 *>(tK + c * LDR + 16 * st + 8 * g2);
+                const h8 ka1 = *reinterpret_cast<const h8 *>(tK + (32 + c) * LDR + 16 * st + 8 * g2);
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    s[qb][0] = mfma32(ka0, qf[qb][st], s[qb][0]);
+                    s[qb][1] = mfma32(ka1, qf[qb][st], s[qb][1]);
+                }
+            }
+
+            // Tail keys (>= S) and the causal triangle -> -inf.
+            const bool need_mask = (k0 + KT > S) || (CAUSAL && k0 + KT - 1 > qw0);
+            if (need_mask) {
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    const int q = qw0 + 32 * qb + c;
+                    const int lim = CAUSAL ? min(q, S - 1) : S - 1;
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                            if (key > lim) s[qb][kb][r] = -INFINITY;
+                        }
+                }
+            }
+
+            h8 pb[QB][2][2];
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                float mx = s[qb][0][0];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
+                mx = fmaxf(mx, xor32(mx));
+                const float mnew = fmaxf(m[qb], mx);
+                float alpha, msc;
+                if (mnew == -INFINITY) {
+                    alpha = 0.f;
+                    msc = 0.f;
+                } else {
+                    alpha = __builtin_amdgcn_exp2f((m[qb] - mnew) * scale2);
+                    msc = mnew * scale2;
+                }
+                m[qb] = mnew;
+                float rs = 0.f;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float p = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r], scale2, -msc));
+                        s[qb][kb][r] = p;
+                        rs += p;
+                    }
+                l[qb] = l[qb] * alpha + rs;
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+                if (DROPOUT) {
+                    const int q = qw0 + 32 * qb + c;
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                            s[qb][kb][r] = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr)
+                                               ? s[qb][kb][r] * a.inv_keep
+                                               : 0.f;
+                        }
+                }
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    pb[qb][kb][0] = acc_to_h8(s[qb][kb], 0);
+                    pb[qb][kb][1] = acc_to_h8(s[qb][kb], 1);
+                }
+            }
+
+            // O^T += V^T P^T, contracting 16 keys per step.
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const h8 va = *reinterpret_cast<const h8 *>(
+                            tVt + (32 * db + c) * LDR + 32 * kb + 16 * hh + 8 * g2);
+#pragma unroll
+                        for (int qb = 0; qb < QB; ++qb)
+                            o[qb][db] = mfma32(va, pb[qb][kb][hh], o[qb][db]);
+                    }
+        }
+
+        if (t + 1 < ntiles) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const float lt = l[qb] + xor32(l[qb]);
+        const int q = qw0 + 32 * qb + c;
+        if (q < S) {
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;
+            _Float16 *orow = Op + q * a.oss;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f4 x;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j] * inv;
+                    *reinterpret_cast<h4 *>(orow + 32 * db + 8 * i + 4 * g2) =
+                        __builtin_convertvector(x, h4);
+                }
+            if (g2 == 0)
+                Lp[q] = (m[qb] == -INFINITY) ? -INFINITY : (m[qb] * scale2 + log2f(lt)) * LN2;
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    const int nqblk = (a.S + QWG - 1) / QWG;
+    const dim3 grid((unsigned)(nqblk * a.B * a.H));
+    const dim3 block(256);
+    if (causal) {
+        if (dropout)
+            hipLaunchKernelGGL((fwd_kernel<true, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((fwd_kernel<true, false>), grid, block, 0, st, a);
+    } else {
+        if (dropout)
+            hipLaunchKernelGGL((fwd_kernel<false, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((fwd_kernel<false, false>), grid, block, 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fa2

@@ -1,0 +1,60 @@
+// fa2_kernels.h -- kernel argument blocks and launch entry points shared by
+// the C ABI layer (fa2_capi.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa2 {
+
+// All strides are in elements.  Kernel-side invariants established by the
+// host (fa2_capi.hip): D == 64, base pointers 16-byte aligned, (b,h,s)
+// strides multiples of 8, scale2 > 0 and finite.
+struct FwdArgs {
+    const _Float16 *q, *k, *v;
+    _Float16 *o;
+    float *lse;
+    int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss, osb, osh, oss, lsb, lsh;
+    int B, H, S;
+    float scale2;        // |softmax_scale| * log2(e), at least FLT_MIN
+    int negate;          // softmax_scale < 0: the Q operand is negated
+    uint32_t seed;       // dropout hash seed
+    uint32_t drop_thr;   // keep iff (hash >> 8) >= drop_thr
+    float inv_keep;      // 1 / (1 - p)
+};
+
+struct BwdArgs {
+    const _Float16 *q, *k, *v, *o, *dout;
+    const float *lse;
+    _Float16 *dq, *dk, *dv;
+    float *delta;        // [B*H, S] fp32 workspace
+    int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss;
+    int64_t osb, osh, oss, dosb, dosh, doss;
+    int64_t dqsb, dqsh, dqss, dksb, dksh, dkss, dvsb, dvsh, dvss;
+    int64_t lsb, lsh;
+    int B, H, S;
+    float scale;         // signed softmax scale (multiplies dQ and dK)
+    float scale2;        // |softmax_scale| * log2(e), at least FLT_MIN
+    int negate;          // softmax_scale < 0: the K operand of S is negated
+    uint32_t seed;
+    uint32_t drop_thr;
+    float inv_keep;
+};
+
+struct RopeArgs {
+    const _Float16 *q, *k;
+    _Float16 *qo, *ko;
+    const float *cs, *sn;
+    int64_t qsb, qsh, qss, ksb, ksh, kss, oqb, oqh, oqs, okb, okh, oks;
+    int64_t cs0, sn0;
+    int B, H, S;
+};
+
+// Launchers; each returns the hipError_t of its launch.
+hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st);
+hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st);
+hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);
+hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);
+hipError_t launch_rope(const RopeArgs &a, bool backward, hipStream_t st);
+
+}  // namespace fa2

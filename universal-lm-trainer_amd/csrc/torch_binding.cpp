@@ -1,0 +1,234 @@
+// torch_binding.cpp -- thin PyTorch-ROCm extension over the C ABI.
+//
+// Exposes the reference's four extension ops with their signatures and
+// output conventions (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:386-397):
+//   fa_fwd(q, k, v, dropout_p, causal, softmax_scale, seed)            -> [o, lse]
+//   fa_bwd(q, k, v, o, lse, do, dropout_p, causal, softmax_scale, seed,
+//          mode=7)                                                      -> [dq, dk, dv]
+//   rope_fwd(q, k, cos, sin)                                            -> [qo, ko]
+//   rope_bwd(dqo, dko, cos, sin, q, k)                                  -> [dq, dk]
+// Inputs are borrowed with their strides; outputs and the backward's delta
+// workspace come from the torch caching allocator on q's device; launches go
+// to the current stream with no host synchronisation.  A nonzero status from
+// the C ABI becomes a RuntimeError carrying the library's message.
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <vector>
+
+#include "../../include/fa2_mi355x.h"
+
+namespace {
+
+void *current_stream(const torch::Tensor &t) {
+    return reinterpret_cast<void *>(at::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
+}
+
+void check_status(int rc, const char *op) {
+    TORCH_CHECK(rc == FA2_OK, op, ": ", fa2_status_string(rc), ": ", fa2_last_error());
+}
+
+void strides3(const torch::Tensor &t, int64_t out[3]) {
+    out[0] = t.stride(0);
+    out[1] = t.stride(1);
+    out[2] = t.stride(2);
+}
+
+// Same contract checks as the reference's check_fwd (flash_attn_v100.cu:314-335).
+void check_qkv(const torch::Tensor &q, const torch::Tensor &k, const torch::Tensor &v) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "inputs must be on the GPU");
+    TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
+                "only fp16 supported");
+    TORCH_CHECK(q.dim() == 4, "q must be (B,H,S,D)");
+    TORCH_CHECK(q.size(3) == 64, "head_dim must be 64");
+    TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(), "q/k/v shape mismatch");
+    TORCH_CHECK(k.device() == q.device() && v.device() == q.device(), "q/k/v device mismatch");
+    TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1, "last dim must be contiguous");
+}
+
+std::vector<torch::Tensor> fa_fwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, double dropout_p, bool causal,
+                                  double softmax_scale, int64_t seed) {
+    check_qkv(q, k, v);
+    at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    const int64_t B = q.size(0), H = q.size(1), S = q.size(2);
+    auto o = torch::empty({B, H, S, 64}, q.options());
+    auto lse = torch::empty({B, H, S}, q.options().dtype(torch::kFloat));
+    fa2_fwd_params p;
+    memset(&p, 0, sizeof(p));
+    p.q = q.data_ptr();
+    p.k = k.data_ptr();
+    p.v = v.data_ptr();
+    p.o = o.data_ptr();
+    p.lse = lse.data_ptr<float>();
+    strides3(q, p.q_stride);
+    strides3(k, p.k_stride);
+    strides3(v, p.v_stride);
+    strides3(o, p.o_stride);
+    p.lse_stride[0] = lse.stride(0);
+    p.lse_stride[1] = lse.stride(1);
+    p.B = (int32_t)B;
+    p.H = (int32_t)H;
+    p.S = (int32_t)S;
+    p.D = 64;
+    p.softmax_scale = (float)softmax_scale;
+    p.dropout_p = (float)dropout_p;
+    p.seed = (uint32_t)seed;
+    p.causal = causal ? 1 : 0;
+    check_status(fa2_fwd_f16(&p, current_stream(q)), "fa_fwd");
+    return {o, lse};
+}
+
+std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor o,
+                                  torch::Tensor lse, torch::Tensor do_, double dropout_p, bool causal,
+                                  double softmax_scale, int64_t seed, int64_t mode) {
+    check_qkv(q, k, v);
+    TORCH_CHECK(o.sizes() == q.sizes() && do_.sizes() == q.sizes(), "o/do shape mismatch");
+    TORCH_CHECK(o.dtype() == torch::kHalf && do_.dtype() == torch::kHalf, "o/do must be fp16");
+    TORCH_CHECK(lse.dtype() == torch::kFloat && lse.dim() == 3 && lse.size(0) == q.size(0) &&
+                    lse.size(1) == q.size(1) && lse.size(2) == q.size(2),
+                "lse must be fp32 (B,H,S)");
+    TORCH_CHECK(mode >= 0 && mode <= 7, "mode must be a bit mask in 0..7");
+    at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    // The kernels take any (b,h,s) strides; only rows must be contiguous and
+    // 16-byte aligned.  lse must have unit stride along s.
+    auto o_c = (o.stride(3) == 1 && o.stride(2) % 8 == 0 && o.stride(1) % 8 == 0 && o.stride(0) % 8 == 0)
+                   ? o
+                   : o.contiguous();
+    auto do_c = (do_.stride(3) == 1 && do_.stride(2) % 8 == 0 && do_.stride(1) % 8 == 0 && do_.stride(0) % 8 == 0)
+                    ? do_
+                    : do_.contiguous();
+    auto lse_c = lse.stride(2) == 1 ? lse : lse.contiguous();
+    const int64_t B = q.size(0), H = q.size(1), S = q.size(2);
+    auto dq = torch::empty({B, H, S, 64}, q.options());
+    auto dk = torch::empty({B, H, S, 64}, q.options());
+    auto dv = torch::empty({B, H, S, 64}, q.options());
+    auto ws = torch::empty({(int64_t)fa2_bwd_workspace_bytes((int32_t)B, (int32_t)H, (int32_t)S) / 4 + 4},
+                           q.options().dtype(torch::kFloat));
+    fa2_bwd_params p;
+    memset(&p, 0, sizeof(p));
+    p.q = q.data_ptr();
+    p.k = k.data_ptr();
+    p.v = v.data_ptr();
+    p.o = o_c.data_ptr();
+    p.dout = do_c.data_ptr();
+    p.lse = lse_c.data_ptr<float>();
+    p.dq = dq.data_ptr();
+    p.dk = dk.data_ptr();
+    p.dv = dv.data_ptr();
+    strides3(q, p.q_stride);
+    strides3(k, p.k_stride);
+    strides3(v, p.v_stride);
+    strides3(o_c, p.o_stride);
+    strides3(do_c, p.do_stride);
+    strides3(dq, p.dq_stride);
+    strides3(dk, p.dk_stride);
+    strides3(dv, p.dv_stride);
+    p.lse_stride[0] = lse_c.stride(0);
+    p.lse_stride[1] = lse_c.stride(1);
+    p.B = (int32_t)B;
+    p.H = (int32_t)H;
+    p.S = (int32_t)S;
+    p.D = 64;
+    p.softmax_scale = (float)softmax_scale;
+    p.dropout_p = (float)dropout_p;
+    p.seed = (uint32_t)seed;
+    p.causal = causal ? 1 : 0;
+    // The workspace is fresh each call, so a dK/dV-only request also computes
+    // delta (the reference would read an uninitialised buffer there).
+    int32_t m = (int32_t)mode;
+    if ((m & 4) && !(m & 3)) m |= 1;
+    check_status(fa2_bwd_f16(&p, m, ws.data_ptr(), (size_t)ws.numel() * 4, current_stream(q)), "fa_bwd");
+    return {dq, dk, dv};
+}
+
+bool is_dense(at::IntArrayRef sizes, at::IntArrayRef strides) {
+    int64_t need = 1, numel = 1;
+    for (size_t i = 0; i < sizes.size(); ++i) {
+        numel *= sizes[i];
+        need += (sizes[i] - 1) * strides[i];
+    }
+    return need == numel;
+}
+
+// Output layout of the eager path (fast_ops.cu:142-150): keep a dense input's
+// strides, (B,S,H,D) order for fused-qkv views, contiguous otherwise.
+std::vector<int64_t> rope_out_strides(const torch::Tensor &x) {
+    if (is_dense(x.sizes(), x.strides())) return x.strides().vec();
+    const int64_t B = x.size(0), H = x.size(1), S = x.size(2), D = x.size(3);
+    (void)B;
+    if (x.stride(1) == D && x.stride(2) >= H * D) return {S * H * D, D, H * D, 1};
+    return {H * S * D, S * D, D, 1};
+}
+
+void rope_check(const torch::Tensor &q, const torch::Tensor &k, const torch::Tensor &cos, const torch::Tensor &sin) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda(), "rope: inputs must be on the GPU");
+    TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf, "rope: fp16 only");
+    TORCH_CHECK(q.dim() == 4 && q.size(3) == 64, "rope: head_dim must be 64");
+    TORCH_CHECK(k.device() == q.device(), "rope: q/k device mismatch");
+    TORCH_CHECK(q.sizes() == k.sizes(), "rope: q/k shape mismatch");
+    TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1, "rope: last dim must be contiguous");
+    TORCH_CHECK(cos.is_cuda() && sin.is_cuda() && cos.dtype() == torch::kFloat && sin.dtype() == torch::kFloat,
+                "rope: cos/sin must be fp32 on the GPU");
+    TORCH_CHECK(cos.device() == q.device() && sin.device() == q.device(), "rope: cos/sin device mismatch");
+    TORCH_CHECK(cos.dim() == 2 && cos.size(0) == q.size(2) && cos.size(1) == 64, "rope: cos/sin must be [S, 64]");
+    TORCH_CHECK(cos.sizes() == sin.sizes(), "rope: cos/sin shape mismatch");
+    TORCH_CHECK(cos.stride(1) == 1 && sin.stride(1) == 1, "rope: cos/sin last dim must be contiguous");
+}
+
+std::vector<torch::Tensor> rope_run(const torch::Tensor &x, const torch::Tensor &y, const torch::Tensor &cos,
+                                    const torch::Tensor &sin, const torch::Tensor &shape_q,
+                                    const torch::Tensor &shape_k, bool backward) {
+    at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    auto qo = torch::empty_strided(shape_q.sizes(), rope_out_strides(shape_q), shape_q.options());
+    auto ko = torch::empty_strided(shape_k.sizes(), rope_out_strides(shape_k), shape_k.options());
+    fa2_rope_params p;
+    memset(&p, 0, sizeof(p));
+    p.q = x.data_ptr();
+    p.k = y.data_ptr();
+    p.qo = qo.data_ptr();
+    p.ko = ko.data_ptr();
+    p.cos = cos.data_ptr<float>();
+    p.sin = sin.data_ptr<float>();
+    strides3(x, p.q_stride);
+    strides3(y, p.k_stride);
+    strides3(qo, p.qo_stride);
+    strides3(ko, p.ko_stride);
+    p.cs_stride = cos.stride(0);
+    p.sn_stride = sin.stride(0);
+    p.B = (int32_t)x.size(0);
+    p.H = (int32_t)x.size(1);
+    p.S = (int32_t)x.size(2);
+    p.D = 64;
+    check_status(fa2_rope_f16(&p, backward ? 1 : 0, current_stream(x)), backward ? "rope_bwd" : "rope_fwd");
+    return {qo, ko};
+}
+
+std::vector<torch::Tensor> rope_fwd(torch::Tensor q, torch::Tensor k, torch::Tensor cos, torch::Tensor sin) {
+    rope_check(q, k, cos, sin);
+    return rope_run(q, k, cos, sin, q, k, false);
+}
+
+std::vector<torch::Tensor> rope_bwd(torch::Tensor dqo, torch::Tensor dko, torch::Tensor cos, torch::Tensor sin,
+                                    torch::Tensor q, torch::Tensor k) {
+    rope_check(q, k, cos, sin);
+    TORCH_CHECK(dqo.sizes() == q.sizes() && dko.sizes() == k.sizes(), "rope_bwd: grad shape");
+    TORCH_CHECK(dqo.is_cuda() && dko.is_cuda() && dqo.dtype() == torch::kHalf && dko.dtype() == torch::kHalf,
+                "rope_bwd: grads must be fp16 on the GPU");
+    TORCH_CHECK(dqo.stride(3) == 1 && dko.stride(3) == 1, "rope_bwd: grad last dim contiguous");
+    return rope_run(dqo, dko, cos, sin, q, k, true);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("fa_fwd", &fa_fwd, "FA2 forward (gfx950 MFMA)");
+    m.def("fa_bwd", &fa_bwd, "FA2 backward (gfx950 MFMA)", pybind11::arg("q"), pybind11::arg("k"),
+          pybind11::arg("v"), pybind11::arg("o"), pybind11::arg("lse"), pybind11::arg("do"),
+          pybind11::arg("dropout_p"), pybind11::arg("causal"), pybind11::arg("softmax_scale"),
+          pybind11::arg("seed"), pybind11::arg("mode") = 7);
+    m.def("rope_fwd", &rope_fwd, "fused RoPE forward");
+    m.def("rope_bwd", &rope_bwd, "fused RoPE backward");
+    m.def("version", []() { return std::string(fa2_version()); });
+}
