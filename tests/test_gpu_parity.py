@@ -41,7 +41,7 @@ def run_kernel(fa, q, k, v, do, causal=True, scale=0.125, p=0.0, seed=0):
     return o, lse, dq, dk, dv
 
 
-def check_against(name, got, ref):
+def check_against(name, got, ref, o_tol=O_TOL):
     o, lse, dq, dk, dv = (t.detach().float().cpu().numpy() for t in got)
     ro, rlse, rdq, rdk, rdv = (np.asarray(x, np.float64) for x in ref)
     eo = orc.max_abs(o, ro)
@@ -50,7 +50,7 @@ def check_against(name, got, ref):
     ma = [orc.max_abs(a, b) for a, b in ((dq, rdq), (dk, rdk), (dv, rdv))]
     say(f"{name}: O maxabs {eo:.2e}  LSE maxabs {el:.2e}  rel dQ/dK/dV {eg[0]:.2e} {eg[1]:.2e} {eg[2]:.2e}"
         f"  maxabs {ma[0]:.2e} {ma[1]:.2e} {ma[2]:.2e}")
-    assert eo <= O_TOL, f"{name}: O max-abs {eo}"
+    assert eo <= o_tol, f"{name}: O max-abs {eo}"
     assert el <= LSE_TOL, f"{name}: LSE max-abs {el}"
     for e, n in zip(eg, ("dQ", "dK", "dV")):
         assert e <= G_TOL, f"{name}: {n} rel err {e}"
@@ -101,7 +101,7 @@ def test_golden_fixtures(fa):
         q, k, v, do = (torch.from_numpy(z[f"{name}/{t}"]).to(DEV) for t in ("q", "k", "v", "do"))
         got = run_kernel(fa, q, k, v, do, causal=bool(causal), scale=float(scale), p=float(p), seed=int(seed))
         ref = [z[f"{name}/{t}"] for t in ("o", "lse", "dq", "dk", "dv")]
-        check_against(f"golden {name}", got, ref)
+        check_against(f"golden {name}", got, ref, o_tol=O_TOL / (1.0 - float(p)))
 
 
 @pytest.mark.parametrize("scale", [0.3, -0.2, 0.0, 0.05])
@@ -117,7 +117,10 @@ def test_dropout_vs_oracle(fa, p, seed):
     say(f"case dropout p={p} seed={seed}")
     q, k, v, do = rand_inputs(2, 2, 160, seed=seed % 1000)
     got = run_kernel(fa, q, k, v, do, p=p, seed=seed)
-    check_against(f"dropout p={p}", got, oracle_ref(q, k, v, do, True, 0.125, p=p, seed=seed))
+    # Dropout scales O by 1/(1-p); the fp16 output's own rounding scales with
+    # it, so the O bar does too (grads keep the relative bar).
+    check_against(f"dropout p={p}", got, oracle_ref(q, k, v, do, True, 0.125, p=p, seed=seed),
+                  o_tol=O_TOL / (1.0 - p))
 
 
 def test_medium_vs_sdpa_math_gpu(fa):
