@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--config", default="2", help="2, 3-512, 3-1024, 3-2048, 3-4096 or 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (3 launches) to calibrate "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
     return ap.parse_args()
 
 
@@ -151,6 +154,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4}))
+        return
     import flash_attn_v100_cuda as fa
     import fa2_capi
     import fa2_workloads as wl

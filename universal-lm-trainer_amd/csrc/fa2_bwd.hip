@@ -59,7 +59,7 @@ constexpr int DQ_KT = 64;                   // keys per tile
 constexpr int DQ_QWG = DQ_NW * 32 * DQ_QB;  // 256 queries per workgroup
 
 template <bool CAUSAL, bool DROPOUT>
-__global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][DQ_KT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sV[2][DQ_KT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sKt[2][HD * LDR];
@@ -258,12 +258,12 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdArgs a) {
 // dK / dV pass
 // ---------------------------------------------------------------------------
 constexpr int KV_NW = 4;
-constexpr int KV_KB = 2;                    // 32-key blocks per wave
+constexpr int KV_KB = 1;                    // 32-key blocks per wave
 constexpr int KV_QT = 64;                   // queries per tile
-constexpr int KV_KWG = KV_NW * 32 * KV_KB;  // 256 keys per workgroup
+constexpr int KV_KWG = KV_NW * 32 * KV_KB;  // keys per workgroup
 
 template <bool CAUSAL, bool DROPOUT>
-__global__ __launch_bounds__(256) void bwd_dkv_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sQ[2][KV_QT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sdO[2][KV_QT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sQt[2][HD * LDR];

@@ -39,6 +39,12 @@ __device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// First MFMA of an accumulation chain: C is the constant zero.
+__device__ __forceinline__ f16x mfma32_first(h8 a, h8 b) {
+    const f16x z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, z, 0, 0, 0);
+}
+
 __device__ __forceinline__ f16x zero16() {
     f16x z;
 #pragma unroll
@@ -73,6 +79,19 @@ __device__ __forceinline__ h8 acc_to_h8(const f16x &acc, int hh) {
 __device__ __forceinline__ h8 neg_h8(h8 v) { return -v; }
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+// acc + sum of the eight halves, two per v_dot2_f32_f16 (fp32 accumulation).
+__device__ __forceinline__ float sum_h8(h8 v, float acc) {
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h2 pr;
+        pr[0] = v[2 * i];
+        pr[1] = v[2 * i + 1];
+        acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+    }
+    return acc;
+}
 
 // Dropout keep decision for element (row = query, col = key) of head bh.
 // The integer function is the reference's (reference @ None:

@@ -20,6 +20,12 @@
 //     per-lane partial until the epilogue, the O^T rescale is a per-lane
 //     scalar, and P goes from the accumulator straight into the B operand of
 //     the PV MFMA (no LDS round trip);
+//   * the reference max used for P is updated lazily (only when a row max
+//     grows by more than 2^8), so the O rescale is almost never executed and
+//     the O accumulators are touched by MFMAs only; row sums use
+//     v_dot2_f32_f16 on the packed fp16 P (2 elements per instruction);
+//   * at most 256 registers per lane, so two waves share each SIMD and one
+//     wave's softmax overlaps the other's MFMAs;
 //   * workgroups are issued heaviest first (last query blocks first) and all
 //     workgroups of one (b, h) share blockIdx % 8, i.e. one XCD and its L2.
 #include "fa2_device.h"
@@ -32,9 +38,10 @@ constexpr int NW = 4;              // waves per workgroup
 constexpr int QB = 2;              // 32-query blocks per wave
 constexpr int KT = 64;             // keys per tile
 constexpr int QWG = NW * 32 * QB;  // queries per workgroup
+constexpr float RESCALE_T = 8.f;   // log2 headroom of the lazy reference max
 
 template <bool CAUSAL, bool DROPOUT>
-__global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][KT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sVt[2][HD * LDR];
 
@@ -72,12 +79,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
     }
 
     f16x o[QB][2];
-    float m[QB], l[QB];
+    float msc[QB], l[QB];   // reference max (log2 units) and per-lane partial row sum
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         o[qb][0] = zero16();
         o[qb][1] = zero16();
-        m[qb] = -INFINITY;
+        msc[qb] = -INFINITY;
         l[qb] = 0.f;
     }
 
@@ -135,18 +142,18 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
             // S^T = K Q^T : s[qb][kb] rows = keys k0 + 32*kb + (8i+4g2+j), col = query.
             f16x s[QB][2];
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) {
-                s[qb][0] = zero16();
-                s[qb][1] = zero16();
-            }
-#pragma unroll
             for (int st = 0; st < 4; ++st) {
                 const h8 ka0 = *reinterpret_cast<const h8 *>(tK + c * LDR + 16 * st + 8 * g2);
                 const h8 ka1 = *reinterpret_cast<const h8 *>(tK + (32 + c) * LDR + 16 * st + 8 * g2);
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
-                    s[qb][0] = mfma32(ka0, qf[qb][st], s[qb][0]);
-                    s[qb][1] = mfma32(ka1, qf[qb][st], s[qb][1]);
+                    if (st == 0) {  // C = inline constant 0: no register zeroing
+                        s[qb][0] = mfma32_first(ka0, qf[qb][st]);
+                        s[qb][1] = mfma32_first(ka1, qf[qb][st]);
+                    } else {
+                        s[qb][0] = mfma32(ka0, qf[qb][st], s[qb][0]);
+                        s[qb][1] = mfma32(ka1, qf[qb][st], s[qb][1]);
+                    }
                 }
             }
 
@@ -167,7 +174,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
                 }
             }
 
-            h8 pb[QB][2][2];
+            // Online softmax with a lazily updated reference max (log2 units,
+            // msc): it moves only when a row max exceeds it by more than
+            // RESCALE_T, so P <= 2^RESCALE_T and the O/l rescale (the only VALU
+            // touch of the O accumulators) is skipped on almost every tile.
+            float tmax[QB];
+            bool grow_any = false;
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 float mx = s[qb][0][0];
@@ -176,46 +188,66 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
                 mx = fmaxf(mx, xor32(mx));
-                const float mnew = fmaxf(m[qb], mx);
-                float alpha, msc;
-                if (mnew == -INFINITY) {
-                    alpha = 0.f;
-                    msc = 0.f;
-                } else {
-                    alpha = __builtin_amdgcn_exp2f((m[qb] - mnew) * scale2);
-                    msc = mnew * scale2;
+                tmax[qb] = mx * scale2;
+                grow_any |= tmax[qb] > msc[qb] + RESCALE_T;
+            }
+            if (__any(grow_any)) {
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    const bool grow = tmax[qb] > msc[qb] + RESCALE_T;
+                    const float alpha = grow ? __builtin_amdgcn_exp2f(msc[qb] - tmax[qb]) : 1.f;
+                    msc[qb] = grow ? tmax[qb] : msc[qb];
+                    l[qb] *= alpha;
+#pragma unroll
+                    for (int db = 0; db < 2; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
                 }
-                m[qb] = mnew;
-                float rs = 0.f;
+            }
+
+            h8 pb[QB][2][2];
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                // msc == -inf only while every key seen so far is masked; then
+                // s == -inf too and P must be 0.
+                const float sub = (msc[qb] == -INFINITY) ? 0.f : msc[qb];
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float p = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r], scale2, -msc));
-                        s[qb][kb][r] = p;
-                        rs += p;
-                    }
-                l[qb] = l[qb] * alpha + rs;
-#pragma unroll
-                for (int db = 0; db < 2; ++db)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+                    for (int r = 0; r < 16; ++r)
+                        s[qb][kb][r] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r], scale2, -sub));
                 if (DROPOUT) {
+                    // the denominator sums the un-dropped P
+                    float rs = 0.f;
                     const int q = qw0 + 32 * qb + c;
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
+                            rs += s[qb][kb][r];
                             const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
                             s[qb][kb][r] = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr)
                                                ? s[qb][kb][r] * a.inv_keep
                                                : 0.f;
                         }
-                }
+                    l[qb] += rs;
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    pb[qb][kb][0] = acc_to_h8(s[qb][kb], 0);
-                    pb[qb][kb][1] = acc_to_h8(s[qb][kb], 1);
+                    for (int kb = 0; kb < 2; ++kb) {
+                        pb[qb][kb][0] = acc_to_h8(s[qb][kb], 0);
+                        pb[qb][kb][1] = acc_to_h8(s[qb][kb], 1);
+                    }
+                } else {
+                    // l sums the same fp16-rounded P that enters the PV MFMA,
+                    // two per v_dot2_f32_f16 with fp32 accumulation.
+                    float rs = 0.f;
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+                        pb[qb][kb][0] = acc_to_h8(s[qb][kb], 0);
+                        pb[qb][kb][1] = acc_to_h8(s[qb][kb], 1);
+                        rs = sum_h8(pb[qb][kb][0], rs);
+                        rs = sum_h8(pb[qb][kb][1], rs);
+                    }
+                    l[qb] += rs;
                 }
             }
 
@@ -256,8 +288,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
                     *reinterpret_cast<h4 *>(orow + 32 * db + 8 * i + 4 * g2) =
                         __builtin_convertvector(x, h4);
                 }
-            if (g2 == 0)
-                Lp[q] = (m[qb] == -INFINITY) ? -INFINITY : (m[qb] * scale2 + log2f(lt)) * LN2;
+            if (g2 == 0) Lp[q] = (msc[qb] == -INFINITY) ? -INFINITY : (msc[qb] + log2f(lt)) * LN2;
         }
     }
 }
