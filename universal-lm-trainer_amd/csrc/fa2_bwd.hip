@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
             h2 pr;
             pr[0] = kr0[e];
             pr[1] = kr1[e];
-            *reinterpret_cast<h2 *>(&sKt[buf][(lc + e) * LDR + pc]) = pr;
+            *reinterpret_cast<h2 *>(&sKt[buf][tpos(lc + e, pc)]) = pr;
         }
     };
 
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
                         const h8 ka = *reinterpret_cast<const h8 *>(
-                            tKt + (32 * db + c) * LDR + 32 * kb + 16 * hh + 8 * g2);
+                            tKt + tpos(32 * db + c, 32 * kb + 16 * hh + 8 * g2));
 #pragma unroll
                         for (int qb = 0; qb < DQ_QB; ++qb) dq[qb][db] = mfma32(ka, dsb[qb][hh], dq[qb][db]);
                     }
@@ -359,8 +359,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
             pq[1] = qr1[e];
             pd[0] = dr0[e];
             pd[1] = dr1[e];
-            *reinterpret_cast<h2 *>(&sQt[buf][(lc + e) * LDR + pc]) = pq;
-            *reinterpret_cast<h2 *>(&sdOt[buf][(lc + e) * LDR + pc]) = pd;
+            *reinterpret_cast<h2 *>(&sQt[buf][tpos(lc + e, pc)]) = pq;
+            *reinterpret_cast<h2 *>(&sdOt[buf][tpos(lc + e, pc)]) = pd;
         }
         if (tid < KV_QT) {
             sL[buf][tid] = lr;
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        const int off = (32 * db + c) * LDR + 32 * qb + 16 * hh + 8 * g2;
+                        const int off = tpos(32 * db + c, 32 * qb + 16 * hh + 8 * g2);
                         const h8 da = *reinterpret_cast<const h8 *>(tdOt + off);
                         const h8 qa = *reinterpret_cast<const h8 *>(tQt + off);
 #pragma unroll

@@ -65,6 +65,16 @@ __device__ __forceinline__ int kperm(int k) {
     return (k & ~0xC) | ((k & 4) << 1) | ((k & 8) >> 1);
 }
 
+// Element offset of (row, col) in a transposed tile [64 rows][LDR] whose
+// columns are in kperm order: the 16-byte chunk index is XOR-swizzled with
+// (row >> 3) & 7.  Rows 8 apart otherwise alias on the same banks (the row
+// stride is 36 dwords), which made the 4-byte transposing stores 8-way bank
+// conflicts; the swizzle spreads them while the 16-byte operand reads (8
+// consecutive rows, one chunk) stay conflict-free.
+__device__ __forceinline__ int tpos(int row, int col) {
+    return row * LDR + ((((col >> 3) ^ (row >> 3)) & 7) << 3) + (col & 7);
+}
+
 // Registers 8*hh .. 8*hh+7 of an accumulator, rounded to fp16 (RNE): the B
 // operand of the next 16-deep MFMA step.
 __device__ __forceinline__ h8 acc_to_h8(const f16x &acc, int hh) {

@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
             h2 pr;
             pr[0] = vr0[e];
             pr[1] = vr1[e];
-            *reinterpret_cast<h2 *>(&sVt[buf][(lc + e) * LDR + pc]) = pr;
+            *reinterpret_cast<h2 *>(&sVt[buf][tpos(lc + e, pc)]) = pr;
         }
     };
 
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
                         const h8 va = *reinterpret_cast<const h8 *>(
-                            tVt + (32 * db + c) * LDR + 32 * kb + 16 * hh + 8 * g2);
+                            tVt + tpos(32 * db + c, 32 * kb + 16 * hh + 8 * g2));
 #pragma unroll
                         for (int qb = 0; qb < QB; ++qb)
                             o[qb][db] = mfma32(va, pb[qb][kb][hh], o[qb][db]);
