@@ -198,6 +198,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
                 for (int qb = 0; qb < DQ_QB; ++qb) {
                     const int q = qw0 + 32 * qb + c;
                     if (need_mask) {
+                        FA2_COLD_BRANCH();
                         const int lim = CAUSAL ? min(q, S - 1) : S - 1;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
@@ -413,15 +414,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
                 }
                 const bool need_mask = CAUSAL && (q0 + 32 * qb < kw0 + 32 * KV_KB - 1);
                 h8 pb[KV_KB][2], dsb[KV_KB][2];
+                if (need_mask) {
+                    FA2_COLD_BRANCH();
+#pragma unroll
+                    for (int kb = 0; kb < KV_KB; ++kb) {
+                        const int key = kw0 + 32 * kb + c;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int q = q0 + 32 * qb + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                            if (key > q) s[kb][r] = -INFINITY;
+                        }
+                    }
+                }
 #pragma unroll
                 for (int kb = 0; kb < KV_KB; ++kb) {
                     const int key = kw0 + 32 * kb + c;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int q = q0 + 32 * qb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                        float sv = s[kb][r];
-                        if (need_mask && key > q) sv = -INFINITY;
-                        const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -l4[r >> 2][r & 3]));
+                        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale2, -l4[r >> 2][r & 3]));
                         const float del = d4[r >> 2][r & 3];
                         float pd = p, ds;
                         if (DROPOUT) {

@@ -39,6 +39,12 @@ __device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Placed first in the body of a rarely taken, wave-uniform branch (causal
+// diagonal masking, lazy rescale): a volatile asm statement cannot be
+// speculated, so the compiler keeps a real branch instead of if-converting the
+// body into selects that would then run on every tile.
+#define FA2_COLD_BRANCH() asm volatile("" ::: "memory")
+
 // First MFMA of an accumulation chain: C is the constant zero.
 __device__ __forceinline__ f16x mfma32_first(h8 a, h8 b) {
     const f16x z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};

@@ -20,10 +20,11 @@
 //     per-lane partial until the epilogue, the O^T rescale is a per-lane
 //     scalar, and P goes from the accumulator straight into the B operand of
 //     the PV MFMA (no LDS round trip);
-//   * the reference max used for P is updated lazily (only when a row max
-//     grows by more than 2^8), so the O rescale is almost never executed and
-//     the O accumulators are touched by MFMAs only; row sums use
-//     v_dot2_f32_f16 on the packed fp16 P (2 elements per instruction);
+//   * no per-tile row max: P is formed against a lazily updated reference
+//     max and an overflow check on its row sum (v_dot2_f32_f16 on the packed
+//     fp16 P) decides when the true max, the O/l rescale and a recompute are
+//     needed, which is almost never after the first tile -- so the O
+//     accumulators are touched by MFMAs only;
 //   * at most 256 registers per lane, so two waves share each SIMD and one
 //     wave's softmax overlaps the other's MFMAs;
 //   * workgroups are issued heaviest first (last query blocks first) and all
@@ -38,7 +39,10 @@ constexpr int NW = 4;              // waves per workgroup
 constexpr int QB = 2;              // 32-query blocks per wave
 constexpr int KT = 64;             // keys per tile
 constexpr int QWG = NW * 32 * QB;  // queries per workgroup
-constexpr float RESCALE_T = 8.f;   // log2 headroom of the lazy reference max
+constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <= 2^15
+#ifndef FA2_FWD_SCHED
+#define FA2_FWD_SCHED 0
+#endif
 
 template <bool CAUSAL, bool DROPOUT>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
@@ -46,7 +50,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sVt[2][HD * LDR];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
+    const int lane = tid & 63, c = lane & 31, g2 = lane >> 5;
     const int S = a.S;
     const int BH = a.B * a.H;
     const int nqblk = (S + QWG - 1) / QWG;
@@ -160,6 +165,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
             // Tail keys (>= S) and the causal triangle -> -inf.
             const bool need_mask = (k0 + KT > S) || (CAUSAL && k0 + KT - 1 > qw0);
             if (need_mask) {
+                FA2_COLD_BRANCH();
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
                     const int q = qw0 + 32 * qb + c;
@@ -174,96 +180,98 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
                 }
             }
 
-            // Online softmax with a lazily updated reference max (log2 units,
-            // msc): it moves only when a row max exceeds it by more than
-            // RESCALE_T, so P <= 2^RESCALE_T and the O/l rescale (the only VALU
-            // touch of the O accumulators) is skipped on almost every tile.
-            float tmax[QB];
-            bool grow_any = false;
+            // Online softmax against a lazily updated reference max msc (log2
+            // units).  P = exp2(s*scale2 - msc) is formed straight away, without
+            // a row max: the lane's fp16 P values are summed (fp32, v_dot2), and
+            // a partial sum <= 2^15 proves no P overflowed fp16.  Only when a
+            // sum exceeds that (or is inf/NaN, as on the first tile where msc =
+            // -inf) does the cold path take the true row max, rescale O and l,
+            // and recompute P.  l and LSE use whatever msc is current, so the
+            // result is the exact online softmax; the reference max only bounds
+            // the magnitudes (P <= 2^15).
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-                float mx = s[qb][0][0];
+                h8 pb[2][2];
+                float rs = 0.f;
+                const float sub = msc[qb];
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
-                mx = fmaxf(mx, xor32(mx));
-                tmax[qb] = mx * scale2;
-                grow_any |= tmax[qb] > msc[qb] + RESCALE_T;
-            }
-            if (__any(grow_any)) {
+                    for (int hh = 0; hh < 2; ++hh) {
+                        f8 x;
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    const bool grow = tmax[qb] > msc[qb] + RESCALE_T;
-                    const float alpha = grow ? __builtin_amdgcn_exp2f(msc[qb] - tmax[qb]) : 1.f;
-                    msc[qb] = grow ? tmax[qb] : msc[qb];
+                        for (int e = 0; e < 8; ++e)
+                            x[e] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][8 * hh + e], scale2, -sub));
+                        pb[kb][hh] = __builtin_convertvector(x, h8);
+                        rs = sum_h8(pb[kb][hh], rs);
+                    }
+                if (__any(!(rs <= P_SUM_LIMIT))) {
+                    FA2_COLD_BRANCH();
+                    float mx = s[qb][0][0];
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
+                    mx = fmaxf(mx, xor32(mx));
+                    const float mnew = fmaxf(msc[qb], mx * scale2);
+                    // mnew == -inf: every key so far masked; alpha stays 1 with O, l = 0
+                    const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc[qb] - mnew);
+                    msc[qb] = mnew;
                     l[qb] *= alpha;
 #pragma unroll
                     for (int db = 0; db < 2; ++db)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+                    const float sub2 = (mnew == -INFINITY) ? 0.f : mnew;
+                    rs = 0.f;
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            f8 x;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e)
+                                x[e] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][8 * hh + e], scale2, -sub2));
+                            pb[kb][hh] = __builtin_convertvector(x, h8);
+                            rs = sum_h8(pb[kb][hh], rs);
+                        }
                 }
-            }
-
-            h8 pb[QB][2][2];
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) {
-                // msc == -inf only while every key seen so far is masked; then
-                // s == -inf too and P must be 0.
-                const float sub = (msc[qb] == -INFINITY) ? 0.f : msc[qb];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        s[qb][kb][r] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][r], scale2, -sub));
                 if (DROPOUT) {
-                    // the denominator sums the un-dropped P
-                    float rs = 0.f;
+                    // l sums the un-dropped P; dropout then zeroes / rescales P.
                     const int q = qw0 + 32 * qb + c;
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            rs += s[qb][kb][r];
-                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                            s[qb][kb][r] = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr)
-                                               ? s[qb][kb][r] * a.inv_keep
-                                               : 0.f;
-                        }
-                    l[qb] += rs;
+                        for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-                        pb[qb][kb][0] = acc_to_h8(s[qb][kb], 0);
-                        pb[qb][kb][1] = acc_to_h8(s[qb][kb], 1);
-                    }
-                } else {
-                    // l sums the same fp16-rounded P that enters the PV MFMA,
-                    // two per v_dot2_f32_f16 with fp32 accumulation.
-                    float rs = 0.f;
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-                        pb[qb][kb][0] = acc_to_h8(s[qb][kb], 0);
-                        pb[qb][kb][1] = acc_to_h8(s[qb][kb], 1);
-                        rs = sum_h8(pb[qb][kb][0], rs);
-                        rs = sum_h8(pb[qb][kb][1], rs);
-                    }
-                    l[qb] += rs;
+                            for (int e = 0; e < 8; ++e) {
+                                const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
+                                const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
+                                pb[kb][hh][e] = keep ? (_Float16)((float)pb[kb][hh][e] * a.inv_keep)
+                                                     : (_Float16)0.f;
+                            }
                 }
+                l[qb] += rs;
+                // O^T += V^T P^T, contracting 16 keys per step.
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const h8 va = *reinterpret_cast<const h8 *>(
+                                tVt + tpos(32 * db + c, 32 * kb + 16 * hh + 8 * g2));
+                            o[qb][db] = mfma32(va, pb[kb][hh], o[qb][db]);
+                        }
             }
-
-            // O^T += V^T P^T, contracting 16 keys per step.
+#if FA2_FWD_SCHED
+            // Interleave: the 16 PV MFMAs each followed by a slice of VALU work.
 #pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const h8 va = *reinterpret_cast<const h8 *>(
-                            tVt + tpos(32 * db + c, 32 * kb + 16 * hh + 8 * g2));
-#pragma unroll
-                        for (int qb = 0; qb < QB; ++qb)
-                            o[qb][db] = mfma32(va, pb[qb][kb][hh], o[qb][db]);
-                    }
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+            }
+#endif
         }
 
         if (t + 1 < ntiles) lstore(buf ^ 1);
