@@ -11,16 +11,17 @@
 // dQ accumulation: split pass, like the reference (its dQ and dK/dV kernels,
 // bwd.cu:66-428), with no atomics:
 //   * bwd_dq_kernel : a workgroup owns 256 queries, keeps Q^T, dO^T, lse and
-//     delta of its queries in registers and streams key tiles (K, V, K^T via
-//     LDS).  It also computes delta itself (the reference's pre-pass,
+//     delta of its queries in registers and streams key tiles (K, V row-major
+//     via LDS; K^T operands come from transposing ds_read_b64_tr_b16 reads).  It also computes delta itself (the reference's pre-pass,
 //     bwd.cu:42-61) from the O and dO rows it holds and stores it for the
 //     dK/dV pass.  S^T and dP^T accumulators give each lane one query, so
 //     lse/delta are per-lane scalars and dS^T feeds the dQ^T = K^T dS^T MFMA
 //     straight from registers.
-//   * bwd_dkv_kernel: a workgroup owns 256 keys (64 per wave, K^T and V^T in
-//     registers), streams query tiles (Q, dO row-major and transposed, lse,
-//     delta via LDS) and accumulates dK^T and dV^T in registers; P and dS
-//     feed the dV/dK MFMAs straight from the S/dP accumulators.
+//   * bwd_dkv_kernel: a workgroup owns 128 keys (32 per wave, K^T and V^T in
+//     registers), streams query tiles (Q, dO row-major, lse, delta via LDS;
+//     Q^T and dO^T operands through transposing reads) and accumulates dK^T
+//     and dV^T in registers; P and dS feed the dV/dK MFMAs straight from the
+//     S/dP accumulators.
 #include "fa2_device.h"
 #include "fa2_kernels.h"
 
@@ -62,7 +63,6 @@ template <bool CAUSAL, bool DROPOUT>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][DQ_KT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sV[2][DQ_KT * LDR];
-    __shared__ __attribute__((aligned(16))) _Float16 sKt[2][HD * LDR];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
@@ -147,14 +147,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
         *reinterpret_cast<h8 *>(&sK[buf][(2 * lp + 1) * LDR + lc]) = kr1;
         *reinterpret_cast<h8 *>(&sV[buf][(2 * lp) * LDR + lc]) = vr0;
         *reinterpret_cast<h8 *>(&sV[buf][(2 * lp + 1) * LDR + lc]) = vr1;
-        const int pc = kperm(2 * lp);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            h2 pr;
-            pr[0] = kr0[e];
-            pr[1] = kr1[e];
-            *reinterpret_cast<h2 *>(&sKt[buf][tpos(lc + e, pc)]) = pr;
-        }
     };
 
     if (ntiles > 0) {
@@ -172,7 +164,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
         if (active) {
             const _Float16 *tK = sK[buf];
             const _Float16 *tV = sV[buf];
-            const _Float16 *tKt = sKt[buf];
             const bool need_mask = (k0 + DQ_KT > S) || (CAUSAL && k0 + DQ_KT - 1 > qw0);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -224,8 +215,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        const h8 ka = *reinterpret_cast<const h8 *>(
-                            tKt + tpos(32 * db + c, 32 * kb + 16 * hh + 8 * g2));
+                        const h8 ka = tr_read8<LDR>(tK, 32 * kb + 16 * hh, 32 * db);
 #pragma unroll
                         for (int qb = 0; qb < DQ_QB; ++qb) dq[qb][db] = mfma32(ka, dsb[qb][hh], dq[qb][db]);
                     }
@@ -267,8 +257,6 @@ template <bool CAUSAL, bool DROPOUT>
 __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sQ[2][KV_QT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sdO[2][KV_QT * LDR];
-    __shared__ __attribute__((aligned(16))) _Float16 sQt[2][HD * LDR];
-    __shared__ __attribute__((aligned(16))) _Float16 sdOt[2][HD * LDR];
     __shared__ __attribute__((aligned(16))) float sL[2][KV_QT];
     __shared__ __attribute__((aligned(16))) float sD[2][KV_QT];
 
@@ -352,17 +340,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
         *reinterpret_cast<h8 *>(&sQ[buf][(2 * lp + 1) * LDR + lc]) = qr1;
         *reinterpret_cast<h8 *>(&sdO[buf][(2 * lp) * LDR + lc]) = dr0;
         *reinterpret_cast<h8 *>(&sdO[buf][(2 * lp + 1) * LDR + lc]) = dr1;
-        const int pc = kperm(2 * lp);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            h2 pq, pd;
-            pq[0] = qr0[e];
-            pq[1] = qr1[e];
-            pd[0] = dr0[e];
-            pd[1] = dr1[e];
-            *reinterpret_cast<h2 *>(&sQt[buf][tpos(lc + e, pc)]) = pq;
-            *reinterpret_cast<h2 *>(&sdOt[buf][tpos(lc + e, pc)]) = pd;
-        }
         if (tid < KV_QT) {
             sL[buf][tid] = lr;
             sD[buf][tid] = drr;
@@ -384,8 +361,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
         if (active) {
             const _Float16 *tQ = sQ[buf];
             const _Float16 *tdO = sdO[buf];
-            const _Float16 *tQt = sQt[buf];
-            const _Float16 *tdOt = sdOt[buf];
 #pragma unroll
             for (int qb = 0; qb < KV_QT / 32; ++qb) {
                 if (CAUSAL && q0 + 32 * qb + 31 < kw0) continue;  // whole block above the diagonal
@@ -455,9 +430,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        const int off = tpos(32 * db + c, 32 * qb + 16 * hh + 8 * g2);
-                        const h8 da = *reinterpret_cast<const h8 *>(tdOt + off);
-                        const h8 qa = *reinterpret_cast<const h8 *>(tQt + off);
+                        const h8 da = tr_read8<LDR>(tdO, 32 * qb + 16 * hh, 32 * db);
+                        const h8 qa = tr_read8<LDR>(tQ, 32 * qb + 16 * hh, 32 * db);
 #pragma unroll
                         for (int kb = 0; kb < KV_KB; ++kb) {
                             dv[kb][db] = mfma32(da, pb[kb][hh], dv[kb][db]);

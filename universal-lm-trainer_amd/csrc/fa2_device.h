@@ -81,6 +81,36 @@ __device__ __forceinline__ int tpos(int row, int col) {
     return row * LDR + ((((col >> 3) ^ (row >> 3)) & 7) << 3) + (col & 7);
 }
 
+// Transposing operand read (ds_read_b64_tr_b16).  From a row-major LDS tile
+// M[k][n] (row stride LD halves), lane 32*g2 + c receives
+//     M[k0 + 8*a + 4*g2 + j][n0 + c]   in slot e = 4*a + j  (a = 0..1, j = 0..3),
+// i.e. the A or B operand of a 16-deep MFMA step whose lane index runs along
+// n and whose k order is the accumulator-chaining order above -- without a
+// transposed copy of the tile.
+// Instruction semantics (measured on gfx950 with an in-bounds probe): within
+// each group of 16 lanes, lane i receives element (i & 3) of the 8-byte
+// segments addressed by lanes 4*e + (i >> 2), e = 0..3.  So source lane s of
+// group G points at row k0 + 8a + 4*(G>>1) + (s>>2), column n0 + 16*(G&1) +
+// 4*(s&3), and two reads (a = 0, 1) fill the 8 slots.  Rows must be 8-byte
+// aligned (LD and n0 multiples of 4).
+typedef short s4v __attribute__((ext_vector_type(4)));
+typedef short s8v __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s4v lds_s4v;
+
+template <int LD>
+__device__ __forceinline__ h8 tr_read8(const _Float16 *tile, int k0, int n0) {
+    const int L = threadIdx.x & 63;
+    const int G = L >> 4, s = L & 15;
+    const int row = k0 + 4 * (G >> 1) + (s >> 2);
+    const int col = n0 + 16 * (G & 1) + 4 * (s & 3);
+    const __attribute__((address_space(3))) _Float16 *t =
+        (const __attribute__((address_space(3))) _Float16 *)tile;
+    const s4v r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + row * LD + col));
+    const s4v r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + (row + 8) * LD + col));
+    const s8v both = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(h8, both);
+}
+
 // Registers 8*hh .. 8*hh+7 of an accumulator, rounded to fp16 (RNE): the B
 // operand of the next 16-deep MFMA step.
 __device__ __forceinline__ h8 acc_to_h8(const f16x &acc, int hh) {

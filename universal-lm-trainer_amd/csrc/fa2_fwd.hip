@@ -11,10 +11,11 @@
 // Work decomposition (one workgroup = 4 waves = 256 queries of one (b, h)):
 //   * each wave owns 64 queries as two 32-query blocks; their Q^T operands
 //     (16 x 32 fp16 per d-step) stay in registers for the whole kernel;
-//   * key tiles of 64 are staged through LDS, double buffered: K row-major
-//     (A operand of S^T = K Q^T) and V transposed with the kperm swizzle
-//     (A operand of O^T = V^T P^T); the next tile's global loads are in
-//     flight while the current tile is computed, one barrier per tile;
+//   * key tiles of 64 are staged row-major through LDS, double buffered: K
+//     feeds the A operand of S^T = K Q^T with 16-byte reads, V feeds the A
+//     operand of O^T = V^T P^T through transposing ds_read_b64_tr_b16 reads;
+//     the next tile's global loads are in flight while the current tile is
+//     computed, one barrier per tile;
 //   * S^T accumulators give each lane one query and 32 keys, so the row max
 //     is a local max plus one cross-half exchange, the running sum l stays a
 //     per-lane partial until the epilogue, the O^T rescale is a per-lane
@@ -47,7 +48,7 @@ constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <
 template <bool CAUSAL, bool DROPOUT>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][KT * LDR];
-    __shared__ __attribute__((aligned(16))) _Float16 sVt[2][HD * LDR];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][KT * LDR];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
@@ -118,14 +119,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
     auto lstore = [&](int buf) {
         *reinterpret_cast<h8 *>(&sK[buf][(2 * lp) * LDR + lc]) = kr0;
         *reinterpret_cast<h8 *>(&sK[buf][(2 * lp + 1) * LDR + lc]) = kr1;
-        const int pc = kperm(2 * lp);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            h2 pr;
-            pr[0] = vr0[e];
-            pr[1] = vr1[e];
-            *reinterpret_cast<h2 *>(&sVt[buf][tpos(lc + e, pc)]) = pr;
-        }
+        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp) * LDR + lc]) = vr0;
+        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp + 1) * LDR + lc]) = vr1;
     };
 
     if (ntiles > 0) {
@@ -142,7 +137,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
         const bool active = (qw0 < S) && (!CAUSAL || k0 <= qw0 + 32 * QB - 1);
         if (active) {
             const _Float16 *tK = sK[buf];
-            const _Float16 *tVt = sVt[buf];
+            const _Float16 *tV = sV[buf];
 
             // S^T = K Q^T : s[qb][kb] rows = keys k0 + 32*kb + (8i+4g2+j), col = query.
             f16x s[QB][2];
@@ -259,8 +254,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
                     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh) {
-                            const h8 va = *reinterpret_cast<const h8 *>(
-                                tVt + tpos(32 * db + c, 32 * kb + 16 * hh + 8 * g2));
+                            const h8 va = tr_read8<LDR>(tV, 32 * kb + 16 * hh, 32 * db);
                             o[qb][db] = mfma32(va, pb[kb][hh], o[qb][db]);
                         }
             }
