@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--config", default="2", help="2, 3-512, 3-1024, 3-2048, 3-4096 or 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
+    ap.add_argument("--bwd-mode", type=int, default=7,
+                    help="fa_bwd mode of the timed step: 7 = split dQ pass (default), "
+                         "15 = fused backward with fp32 dQ atomics")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (3 launches) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
@@ -190,7 +193,7 @@ def main():
 
     def step():
         o, lse = ext.fa_fwd(q, k, v, 0.0, True, scale, 0)
-        ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, scale, 0, 7)
+        ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, scale, 0, args.bwd_mode)
 
     for _ in range(args.warmup):
         step()
@@ -251,7 +254,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"causal FA-2 fwd+bwd, config {args.config}: B={B} H={H} S={S} D=64 fp16"
                                + (" RoPE inputs" if cfg["rope"] else ""),
-                   "B": B, "H": H, "S": S, "D": 64, "algorithmic_gflop_per_step": round(step_flops / 1e9, 2)},
+                   "B": B, "H": H, "S": S, "D": 64, "algorithmic_gflop_per_step": round(step_flops / 1e9, 2),
+                   "bwd_mode": args.bwd_mode},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": round(PEAK_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(dom)},
         "kernels": kernels,

@@ -62,15 +62,20 @@ typedef struct fa2_fwd_params {
 int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
 
 /* Backward: dQ, dK, dV from Q, K, V, O, LSE and dO, recomputing P from LSE.
- * delta[b,h,i] = sum_d O*dO (fp32) is produced inside the dQ pass and kept in
- * the workspace for the dK/dV pass.
  * Replaces fav100::fa_bwd and its three kernels (delta, dQ, dK/dV)
  *   (reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:42-506).
- * `mode` keeps the reference's bit mask (bwd.cu:476-502):
- *   bit 1 = delta, bit 2 = dQ, bit 4 = dK/dV; 7 = all.  Here delta is fused
- *   into the dQ pass, so bit 1 alone computes delta only, bit 2 computes delta
- *   and dQ, and bit 4 without bit 1 or 2 reads delta left in the workspace by
- *   an earlier call. */
+ * `mode` keeps the reference's bit mask (bwd.cu:476-502), 1 = delta,
+ * 2 = dQ, 4 = dK/dV, 7 = all, plus bit 8:
+ *   - 7: split pass like the reference -- a dQ kernel that also writes delta,
+ *     then the dK/dV kernel (no atomics, run-to-run identical);
+ *   - 2: the dQ kernel (writes delta); 1: delta only; 4: dK/dV reading the
+ *     delta an earlier call left in the workspace;
+ *   - 14 or 15 (bit 8 with dQ and dK/dV): fused backward -- delta and a
+ *     cleared fp32 dQ accumulator, one dK/dV kernel that also adds dS K into
+ *     the accumulator with fp32 atomics, then dQ = scale * accumulator.
+ *     Slower on MI355X (the atomics are L2-throughput bound); kept selectable.
+ * The workspace (fa2_bwd_workspace_bytes) holds delta[b,h,i] = sum_d O*dO in
+ * fp32 and the fp32 dQ accumulator. */
 typedef struct fa2_bwd_params {
     const void *q, *k, *v, *o, *dout;   /* fp16 [B,H,S,64]                     */
     const float *lse;                   /* fp32 [B,H,S] from the forward       */
@@ -85,7 +90,8 @@ typedef struct fa2_bwd_params {
     int32_t causal;
 } fa2_bwd_params;
 
-/* Workspace bytes fa2_bwd_f16 needs for (B, H, S): the fp32 delta rows. */
+/* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta (4*B*H*S bytes,
+ * rounded up to 256) followed by the fp32 dQ accumulator (256*B*H*S bytes). */
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S);
 
 int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,

@@ -81,7 +81,8 @@ def test_empty_problem_is_a_noop():
     for dim in ("B", "H", "S"):
         p = _dummy_fwd(**{dim: 0})
         assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 0
-    assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 2 * 3 * 5 * 4
+    # fp32 delta rounded up to 256 bytes, then the fp32 dQ accumulator
+    assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 256 + 2 * 3 * 5 * 64 * 4
     assert lib.fa2_bwd_workspace_bytes(0, 3, 5) == 0
 
 
@@ -89,7 +90,7 @@ def test_bwd_validation():
     lib = capi.load()
     p = capi.BwdParams()
     p.B, p.H, p.S, p.D, p.softmax_scale = 1, 1, 64, 64, 0.125
-    assert lib.fa2_bwd_f16(ctypes.byref(p), 9, None, 0, None) == 4          # bad mode
+    assert lib.fa2_bwd_f16(ctypes.byref(p), 16, None, 0, None) == 4         # bad mode
     assert lib.fa2_bwd_f16(ctypes.byref(p), 7, None, 0, None) == 5          # no workspace
     assert lib.fa2_bwd_f16(ctypes.byref(p), 7, ctypes.c_void_p(1 << 20), 16, None) == 5  # too small
     assert lib.fa2_bwd_f16(ctypes.byref(p), 0, None, 0, None) == 0          # nothing requested

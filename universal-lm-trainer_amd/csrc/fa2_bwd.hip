@@ -49,6 +49,32 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const BwdArgs a) {
     sum += __shfl_xor(sum, 2);
     sum += __shfl_xor(sum, 4);
     if (row < S && part == 0) a.delta[(int64_t)bh * S + row] = sum;
+    if (a.dqacc && row < S) {  // fused backward: clear this row of the fp32 dQ accumulator
+        f4 *z = reinterpret_cast<f4 *>(a.dqacc + ((int64_t)bh * S + row) * HD + 8 * part);
+        const f4 zero = {0.f, 0.f, 0.f, 0.f};
+        z[0] = zero;
+        z[1] = zero;
+    }
+}
+
+// dQ = fp16(scale * accumulator), 8 lanes per row (fused backward epilogue).
+__global__ __launch_bounds__(256) void bwd_dq_convert_kernel(const BwdArgs a) {
+    const int S = a.S;
+    const int nrb = (S + 31) / 32;
+    const int bh = blockIdx.x / nrb;
+    const int row = (blockIdx.x - bh * nrb) * 32 + (threadIdx.x >> 3);
+    if (row >= S) return;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int part = threadIdx.x & 7;
+    const f4 *src = reinterpret_cast<const f4 *>(a.dqacc + ((int64_t)bh * S + row) * HD + 8 * part);
+    const f4 x0 = src[0], x1 = src[1];
+    f8 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        y[e] = x0[e] * a.scale;
+        y[4 + e] = x1[e] * a.scale;
+    }
+    *reinterpret_cast<h8 *>(a.dq + b * a.dqsb + h * a.dqsh + row * a.dqss + 8 * part) = __builtin_convertvector(y, h8);
 }
 
 // ---------------------------------------------------------------------------
@@ -253,12 +279,16 @@ constexpr int KV_KB = 1;                    // 32-key blocks per wave
 constexpr int KV_QT = 64;                   // queries per tile
 constexpr int KV_KWG = KV_NW * 32 * KV_KB;  // keys per workgroup
 
-template <bool CAUSAL, bool DROPOUT>
+template <bool CAUSAL, bool DROPOUT, bool FUSE>
 __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sQ[2][KV_QT * LDR];
     __shared__ __attribute__((aligned(16))) _Float16 sdO[2][KV_QT * LDR];
     __shared__ __attribute__((aligned(16))) float sL[2][KV_QT];
     __shared__ __attribute__((aligned(16))) float sD[2][KV_QT];
+    // Fused dQ: K rows of this workgroup's keys (B operand of dQ = dS K) and the
+    // tile's dS^T [key][query] (A operand, read transposed).
+    __shared__ __attribute__((aligned(16))) _Float16 sKw[FUSE ? KV_KWG * LDR : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 sdSt[FUSE ? KV_KWG * LDR : 8];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
@@ -346,6 +376,26 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
         }
     };
 
+    if (FUSE) {
+        // K rows [k_wg0, k_wg0 + KV_KWG) into LDS, zero past S (un-negated K: dQ = scale dS K).
+#pragma unroll
+        for (int it = 0; it < KV_KWG * 8 / 256; ++it) {
+            const int idx = tid + 256 * it;
+            const int r = idx >> 3, ch = (idx & 7) * 8;
+            h8 kv = zero_h8();
+            if (k_wg0 + r < S) kv = *reinterpret_cast<const h8 *>(Kp + (k_wg0 + r) * a.kss + ch);
+            *reinterpret_cast<h8 *>(&sKw[r * LDR + ch]) = kv;
+        }
+    }
+    // dS^T rows of this lane's key for query block qb (zeros where nothing is computed)
+    _Float16 *dst_row = sdSt + (FUSE ? (32 * wave + c) * LDR : 0);
+    auto write_ds_zero = [&](int qb) {
+        const h4 z = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<h4 *>(dst_row + 32 * qb + 8 * i + 4 * g2) = z;
+    };
+    const bool key_valid = kw0 + c < S;
+
     if (ntiles > 0) {
         gload(q_start);
         lstore(0);
@@ -358,12 +408,19 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
         if (t + 1 < ntiles) gload(q0 + KV_QT);
 
         const bool active = (kw0 < S) && (!CAUSAL || q0 + KV_QT - 1 >= kw0);
+        if (FUSE && !active) {
+            write_ds_zero(0);
+            write_ds_zero(1);
+        }
         if (active) {
             const _Float16 *tQ = sQ[buf];
             const _Float16 *tdO = sdO[buf];
 #pragma unroll
             for (int qb = 0; qb < KV_QT / 32; ++qb) {
-                if (CAUSAL && q0 + 32 * qb + 31 < kw0) continue;  // whole block above the diagonal
+                if (CAUSAL && q0 + 32 * qb + 31 < kw0) {  // whole block above the diagonal
+                    if (FUSE) write_ds_zero(qb);
+                    continue;
+                }
                 // S = Q K^T and dP = dO V^T : rows = queries, cols = this lane's key.
                 f16x s[KV_KB], dp[KV_KB];
 #pragma unroll
@@ -425,6 +482,18 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
                     dsb[kb][0] = acc_to_h8(dp[kb], 0);
                     dsb[kb][1] = acc_to_h8(dp[kb], 1);
                 }
+                if (FUSE) {
+                    // dS^T[key][q]: registers 8hh..8hh+7 hold queries 16hh + 8*(e>>2) + 4*g2 + (e&3)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        h8 v = dsb[0][hh];
+                        if (!key_valid) v = zero_h8();
+                        const h4 lo = {v[0], v[1], v[2], v[3]};
+                        const h4 hi = {v[4], v[5], v[6], v[7]};
+                        *reinterpret_cast<h4 *>(dst_row + 32 * qb + 16 * hh + 4 * g2) = lo;
+                        *reinterpret_cast<h4 *>(dst_row + 32 * qb + 16 * hh + 8 + 4 * g2) = hi;
+                    }
+                }
                 // dV^T += dO^T P and dK^T += Q^T dS, contracting 16 queries per step.
 #pragma unroll
                 for (int db = 0; db < 2; ++db)
@@ -441,6 +510,27 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
             }
         }
 
+        if (FUSE) {
+            // dQ[q0 .. q0+63][0..63] += dS[64 x KV_KWG] K[KV_KWG x 64]: one 32x32 block per
+            // wave over all of this workgroup's keys, added to the fp32 accumulator.
+            __syncthreads();  // every wave's dS^T is in LDS
+            const int qb2 = wave >> 1, db = wave & 1;
+            f16x acc;
+#pragma unroll
+            for (int ks = 0; ks < KV_KWG / 16; ++ks) {
+                const h8 da = tr_read8<LDR>(sdSt, 16 * ks, 32 * qb2);
+                const h8 kb8 = tr_read8<LDR>(sKw, 16 * ks, 32 * db);
+                acc = ks == 0 ? mfma32_first(da, kb8) : mfma32(da, kb8, acc);
+            }
+            float *accrow = a.dqacc + ((int64_t)bh * S + q0 + 32 * qb2) * HD + 32 * db + c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = 8 * i + 4 * g2 + j;
+                    if (q0 + 32 * qb2 + r < S) atomicAddNoRet(accrow + r * HD, acc[4 * i + j]);
+                }
+        }
         if (t + 1 < ntiles) lstore(buf ^ 1);
         __syncthreads();
     }
@@ -494,20 +584,36 @@ hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+template <bool FUSE>
+static void launch_dkv_t(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const int nkblk = (a.S + KV_KWG - 1) / KV_KWG;
     const dim3 grid((unsigned)(nkblk * a.B * a.H)), block(256);
     if (causal) {
         if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_kernel<true, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_kernel<true, true, FUSE>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dkv_kernel<true, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_kernel<true, false, FUSE>), grid, block, 0, st, a);
     } else {
         if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_kernel<false, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_kernel<false, true, FUSE>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dkv_kernel<false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_kernel<false, false, FUSE>), grid, block, 0, st, a);
     }
+}
+
+hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    launch_dkv_t<false>(a, causal, dropout, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_fused(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    launch_dkv_t<true>(a, causal, dropout, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_dq_convert(const BwdArgs &a, hipStream_t st) {
+    const int nrb = (a.S + 31) / 32;
+    hipLaunchKernelGGL(bwd_dq_convert_kernel, dim3((unsigned)(nrb * a.B * a.H)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

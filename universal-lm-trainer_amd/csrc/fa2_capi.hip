@@ -128,15 +128,21 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
     return FA2_OK;
 }
 
+// Workspace: fp32 delta [B*H*S] (rounded up to 256 bytes), then the fp32 dQ
+// accumulator [B*H*S*64] of the fused backward.
+static size_t delta_bytes(int32_t B, int32_t H, int32_t S) {
+    return ((size_t)B * H * S * sizeof(float) + 255) & ~(size_t)255;
+}
+
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S) {
     if (B <= 0 || H <= 0 || S <= 0) return 0;
-    return (size_t)B * H * S * sizeof(float);
+    return delta_bytes(B, H, S) + (size_t)B * H * S * FA2_HEAD_DIM * sizeof(float);
 }
 
 int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t workspace_bytes, void *stream) {
     g_err[0] = 0;
     if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
-    if (mode < 0 || mode > 7) return fail(FA2_ERR_BAD_ARGUMENT, "mode %d outside 0..7", mode);
+    if (mode < 0 || mode > 15) return fail(FA2_ERR_BAD_ARGUMENT, "mode %d outside 0..15", mode);
     int rc = check_shape(p->B, p->H, p->S, p->D, 256);
     if (rc) return rc;
     if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
@@ -147,6 +153,7 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     if (reinterpret_cast<uintptr_t>(workspace) & 15u)
         return fail(FA2_ERR_MISALIGNED, "workspace is not 16-byte aligned");
     const bool want_delta = mode & 1, want_dq = mode & 2, want_dkv = mode & 4;
+    const bool fused = want_dq && want_dkv && (mode & 8);
     if ((rc = check_tensor("o", p->o, p->o_stride, p->B, p->H, p->S, true))) return rc;
     if ((rc = check_tensor("dout", p->dout, p->do_stride, p->B, p->H, p->S, true))) return rc;
     if (want_dq || want_dkv) {
@@ -179,6 +186,8 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     a.dk = static_cast<_Float16 *>(p->dk);
     a.dv = static_cast<_Float16 *>(p->dv);
     a.delta = static_cast<float *>(workspace);
+    a.dqacc = fused ? reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S))
+                    : nullptr;
     a.qsb = p->q_stride[0]; a.qsh = p->q_stride[1]; a.qss = p->q_stride[2];
     a.ksb = p->k_stride[0]; a.ksh = p->k_stride[1]; a.kss = p->k_stride[2];
     a.vsb = p->v_stride[0]; a.vsh = p->v_stride[1]; a.vss = p->v_stride[2];
@@ -199,6 +208,16 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     const hipStream_t st = (hipStream_t)stream;
 
     hipError_t e = hipSuccess;
+    if (fused) {
+        // delta + cleared accumulator, then dK/dV with dQ accumulated by atomics, then dQ = scale * acc
+        e = fa2::launch_bwd_delta(a, st);
+        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "delta launch: %s", hipGetErrorString(e));
+        e = fa2::launch_bwd_fused(a, causal, dropout, st);
+        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "fused backward launch: %s", hipGetErrorString(e));
+        e = fa2::launch_bwd_dq_convert(a, st);
+        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "dQ convert launch: %s", hipGetErrorString(e));
+        return FA2_OK;
+    }
     if (want_dq) {
         e = fa2::launch_bwd_dq(a, causal, dropout, st);  // also writes delta
         if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "dQ launch: %s", hipGetErrorString(e));

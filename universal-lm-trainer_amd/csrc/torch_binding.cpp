@@ -89,7 +89,7 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     TORCH_CHECK(lse.dtype() == torch::kFloat && lse.dim() == 3 && lse.size(0) == q.size(0) &&
                     lse.size(1) == q.size(1) && lse.size(2) == q.size(2),
                 "lse must be fp32 (B,H,S)");
-    TORCH_CHECK(mode >= 0 && mode <= 7, "mode must be a bit mask in 0..7");
+    TORCH_CHECK(mode >= 0 && mode <= 15, "mode must be a bit mask in 0..15");
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     // The kernels take any (b,h,s) strides; only rows must be contiguous and
     // 16-byte aligned.  lse must have unit stride along s.
@@ -104,7 +104,7 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     auto dq = torch::empty({B, H, S, 64}, q.options());
     auto dk = torch::empty({B, H, S, 64}, q.options());
     auto dv = torch::empty({B, H, S, 64}, q.options());
-    auto ws = torch::empty({(int64_t)fa2_bwd_workspace_bytes((int32_t)B, (int32_t)H, (int32_t)S) / 4 + 4},
+    auto ws = torch::empty({(int64_t)fa2_bwd_workspace_bytes((int32_t)B, (int32_t)H, (int32_t)S) / 4 + 64},
                            q.options().dtype(torch::kFloat));
     fa2_bwd_params p;
     memset(&p, 0, sizeof(p));
