@@ -41,7 +41,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="2", help="2, 3-512, 3-1024, 3-2048, 3-4096 or 4")
+    ap.add_argument("--config", default="2",
+                    help="2, 3-512, 3-1024, 3-2048, 3-4096, 4, or 5 (10-layer decoder training step "
+                         "with attention timed inside it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
     ap.add_argument("--bwd-mode", type=int, default=7,
@@ -147,6 +149,99 @@ def cpu_baseline():
     }
 
 
+def decoder_step(args, torch, fa):
+    """Configuration 5: one training step of a 10-layer, 100M-preset decoder
+    (d_model 768, 12 heads, SwiGLU 2048, tied head over vocab 32000), B=4,
+    S=4096, fp16 autocast, GradScaler, gradient clipping and fused AdamW as in
+    the reference loop (reference @ None: train.py:2188-2197, 2219, 2341-2424).
+    Attention fwd and bwd are timed inside the step with HIP events around each
+    launch on the launch stream; the attention rate is its algorithmic flops
+    over that time."""
+    import fa2_decoder as dec
+    B, S, L = 4, 4096, 10
+    ext = fa.extension()
+    torch.manual_seed(0)
+    model = dec.Decoder(n_layers=L, fa=fa).cuda()
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.1, betas=(0.9, 0.95), fused=True)
+    scaler = torch.amp.GradScaler("cuda")
+    ids = dec.synthetic_ids(B, S, seed=0, device="cuda")
+    spans = []          # (start, end) events of every attention launch while recording
+    rec = [False]
+
+    def timed(fn):
+        if not rec[0]:
+            return fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = fn()
+        e1.record()
+        spans.append((e0, e1))
+        return out
+
+    class TimedAttention(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, q, k, v):
+            o, lse = timed(lambda: ext.fa_fwd(q, k, v, 0.0, True, 0.125, 0))
+            ctx.save_for_backward(q, k, v, o, lse)
+            return o
+
+        @staticmethod
+        def backward(ctx, do):
+            q, k, v, o, lse = ctx.saved_tensors
+            do = do if do.stride(3) == 1 else do.contiguous()
+            dq, dk, dv = timed(lambda: ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, 0.125, 0, args.bwd_mode))
+            return dq, dk, dv
+
+    for layer in model.layers:
+        layer.attn.attn_fn = TimedAttention.apply
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = model.loss(ids)
+        scaler.scale(loss).backward()
+        scaler.unscale_(opt)
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        scaler.step(opt)
+        scaler.update()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    rec[0] = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    rec[0] = False
+    attn_ms = sum(a.elapsed_time(b) for a, b in spans) / args.steps
+    assert len(spans) == 2 * L * args.steps, len(spans)
+    attn_flops = dec.step_flops_attention(B, S, n_layers=L)
+    value = attn_flops / (attn_ms / 1e3) / 1e12
+    ms_per_step = elapsed / args.steps * 1e3
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (seeded uniform token ids, random-init weights)",
+        "config": {"workload": f"config 5: {L}-layer decoder training step (d_model 768, 12 heads, SwiGLU 2048, "
+                               f"vocab 32000, tied head) B={B} S={S}, fp16 autocast + GradScaler + fused AdamW; "
+                               f"value = attention fwd+bwd rate inside the step",
+                   "B": B, "S": S, "layers": L, "bwd_mode": args.bwd_mode},
+        "step": {"tokens_per_s": round(B * S / (ms_per_step / 1e3), 1),
+                 "attention_ms_per_step": round(attn_ms, 3),
+                 "attention_share": round(attn_ms / ms_per_step, 4),
+                 "approx_model_tflops": round(dec.approx_step_flops(B, S) / (ms_per_step / 1e3) / 1e12, 1),
+                 "last_loss": round(float(loss), 4)},
+    }
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -173,6 +268,9 @@ def main():
     if not fa.is_available():
         raise SystemExit(f"native extension not loaded: {fa.build_error()}")
     ext = fa.extension()
+    if args.config == "5":
+        print(json.dumps(decoder_step(args, torch, fa)), flush=True)
+        return
     key = cfg_key(args.config)
     cfg = wl.CONFIGS[key]
     B, H, S = cfg["B"], cfg["H"], cfg["S"]

@@ -7,9 +7,10 @@
 //          mode=7)                                                      -> [dq, dk, dv]
 //   rope_fwd(q, k, cos, sin)                                            -> [qo, ko]
 //   rope_bwd(dqo, dko, cos, sin, q, k)                                  -> [dq, dk]
-// Inputs are borrowed with their strides; outputs and the backward's delta
-// workspace come from the torch caching allocator on q's device; launches go
-// to the current stream with no host synchronisation.  A nonzero status from
+// Inputs are borrowed with their strides; outputs and the backward's
+// workspace come from the torch caching allocator on q's device (fa_fwd's O
+// follows q's memory order, see fa_fwd); launches go to the current stream
+// with no host synchronisation.  A nonzero status from
 // the C ABI becomes a RuntimeError carrying the library's message.
 #include <torch/extension.h>
 
@@ -53,7 +54,15 @@ std::vector<torch::Tensor> fa_fwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     check_qkv(q, k, v);
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     const int64_t B = q.size(0), H = q.size(1), S = q.size(2);
-    auto o = torch::empty({B, H, S, 64}, q.options());
+    // O follows q's memory order the way an eager elementwise output would:
+    // for the (B,S,H,D) layout train.py produces (q.stride(1) == 64,
+    // q.stride(2) >= H*64) O is stored as [B,S,H,64] and returned as the
+    // (B,H,S,64) view, so the caller's transpose(1,2).contiguous() is free;
+    // otherwise O is contiguous (B,H,S,64) as in the reference
+    // (flash_attn_v100.cu:342).
+    const bool bshd = q.stride(1) == 64 && q.stride(2) >= H * 64 && H > 1;
+    auto o = bshd ? torch::empty({B, S, H, 64}, q.options()).transpose(1, 2)
+                  : torch::empty({B, H, S, 64}, q.options());
     auto lse = torch::empty({B, H, S}, q.options().dtype(torch::kFloat));
     fa2_fwd_params p;
     memset(&p, 0, sizeof(p));

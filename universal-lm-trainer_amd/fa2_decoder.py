@@ -1,0 +1,112 @@
+"""Minimal pre-norm decoder in the reference's shape, used to exercise the
+attention path inside a full training step (benchmark configuration 5) and in
+the model-level drop-in test.
+
+It mirrors what reaches the attention kernel in the reference
+(reference @ None: train.py:1861-2105) -- fused QKV projection, q/k/v as
+(B,S,H,D) views transposed to (B,H,S,D), fused RoPE through
+``flash_attn_v100_cuda.rope`` (eager fallback otherwise), attention through
+``flash_attn_v100_cuda.flash_attn_v100`` (SDPA fallback otherwise),
+``attn.transpose(1,2).contiguous().view(B,S,D)`` and the output projection --
+plus RMSNorm, a SwiGLU FFN and a tied LM head.  It is a consumer of the path,
+not a reimplementation of the reference's training runtime.
+"""
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+import fa2_workloads as wl
+
+
+def rotate_half(x):
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat((-x2, x1), dim=-1)
+
+
+class Attention(nn.Module):
+    def __init__(self, d_model, n_heads, fa=None, use_kernel=True):
+        super().__init__()
+        self.h, self.d = n_heads, d_model // n_heads
+        self.wqkv = nn.Linear(d_model, 3 * d_model, bias=False)
+        self.wo = nn.Linear(d_model, d_model, bias=False)
+        self.fa, self.use_kernel = fa, use_kernel
+        self.attn_fn = None  # optional override (q, k, v) -> o, used for timing
+
+    def forward(self, x, cos, sin):
+        B, S, D = x.shape
+        q, k, v = self.wqkv(x).chunk(3, dim=-1)
+        q = q.view(B, S, self.h, self.d).transpose(1, 2)
+        k = k.view(B, S, self.h, self.d).transpose(1, 2)
+        v = v.view(B, S, self.h, self.d).transpose(1, 2)
+        fa = self.fa if self.use_kernel else None
+        if fa is not None and fa.rope_can_use(q, k, cos, sin):
+            q, k = fa.rope(q, k, cos, sin)
+        else:
+            c, s = cos[None, None], sin[None, None]
+            q, k = q * c + rotate_half(q) * s, k * c + rotate_half(k) * s
+        if torch.is_autocast_enabled():
+            q, k, v = (t.half() if t.dtype == torch.float32 else t for t in (q, k, v))
+        if fa is not None and fa.can_use(q, k, v):
+            attn = self.attn_fn(q, k, v) if self.attn_fn else fa.flash_attn_v100(q, k, v, causal=True)
+        else:
+            attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        return self.wo(attn.transpose(1, 2).contiguous().view(B, S, D))
+
+
+class Block(nn.Module):
+    def __init__(self, d_model, n_heads, d_ff, fa, use_kernel):
+        super().__init__()
+        self.n1 = nn.RMSNorm(d_model, eps=1e-6)
+        self.n2 = nn.RMSNorm(d_model, eps=1e-6)
+        self.attn = Attention(d_model, n_heads, fa, use_kernel)
+        self.w1 = nn.Linear(d_model, d_ff, bias=False)
+        self.w3 = nn.Linear(d_model, d_ff, bias=False)
+        self.w2 = nn.Linear(d_ff, d_model, bias=False)
+
+    def forward(self, x, cos, sin):
+        x = x + self.attn(self.n1(x), cos, sin)
+        h = self.n2(x)
+        return x + self.w2(F.silu(self.w1(h)) * self.w3(h))
+
+
+class Decoder(nn.Module):
+    def __init__(self, vocab=32000, d_model=768, n_heads=12, n_layers=10, d_ff=2048, fa=None, use_kernel=True):
+        super().__init__()
+        self.emb = nn.Embedding(vocab, d_model)
+        self.layers = nn.ModuleList(Block(d_model, n_heads, d_ff, fa, use_kernel) for _ in range(n_layers))
+        self.norm = nn.RMSNorm(d_model, eps=1e-6)
+        self.head_dim = d_model // n_heads
+        self.d_model = d_model
+        for p in self.parameters():  # std 0.02 init (train.py:2015-2022)
+            nn.init.normal_(p, std=0.02) if p.dim() > 1 else nn.init.ones_(p)
+
+    def forward(self, ids):
+        S = ids.shape[1]
+        cos, sin = wl.rope_tables(S, d_model=self.d_model, head_dim=self.head_dim)
+        cos, sin = cos.to(ids.device), sin.to(ids.device)
+        x = self.emb(ids)
+        for layer in self.layers:
+            x = layer(x, cos, sin)
+        return F.linear(self.norm(x), self.emb.weight)  # tied head
+
+    def loss(self, ids):
+        logits = self.forward(ids[:, :-1])
+        return F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), ids[:, 1:].reshape(-1))
+
+
+def synthetic_ids(B, S, vocab=32000, seed=0, device="cpu"):
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randint(0, vocab, (B, S + 1), generator=g).to(device)
+
+
+def step_flops_attention(B, S, H=12, D=64, n_layers=10):
+    f, b = wl.causal_flops(B, H, S, D)
+    return n_layers * (f + b)
+
+
+def approx_step_flops(B, S, d_model=768, d_ff=2048, n_layers=10, vocab=32000):
+    """6 * params_active * tokens for the linear layers and head, plus attention."""
+    lin = n_layers * (4 * d_model * d_model + 3 * d_model * d_ff) + vocab * d_model
+    return 6 * lin * B * S + step_flops_attention(B, S, d_model // 64, 64, n_layers)
+
