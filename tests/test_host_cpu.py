@@ -64,7 +64,8 @@ def _dummy_fwd(**kw):
 
 @pytest.mark.parametrize("field,value,status", [
     ("D", 128, 2), ("S", -1, 2), ("q", 0, 1), ("lse", 0, 1), ("k", (1 << 20) + 8, 3),
-    ("v_stride", capi.I64x3(64 * 8 * 16, 64 * 16, 68), 3), ("dropout_p", 1.0, 4),
+    ("v_stride", capi.I64x3(64 * 8 * 16, 64 * 16, 68), 3), ("q_stride", capi.I64x3(0, 0, 1 << 24), 2),
+    ("dropout_p", 1.0, 4),
     ("dropout_p", -0.1, 4), ("softmax_scale", float("nan"), 4),
 ])
 def test_fwd_validation_rejects_before_launch(field, value, status):

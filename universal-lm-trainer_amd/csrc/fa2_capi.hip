@@ -37,6 +37,9 @@ int check_tensor(const char *name, const void *ptr, const int64_t st[3], int32_t
         if (!vec16 && (st[i] % 2) != 0)
             return fail(FA2_ERR_MISALIGNED, "%s stride[%d] = %lld is odd", name, i, (long long)st[i]);
     }
+    // Kernels address a 64-row tile with 32-bit byte offsets from its first row.
+    if (st[2] >= (1 << 24))
+        return fail(FA2_ERR_BAD_SHAPE, "%s sequence stride %lld is not below 2^24 elements", name, (long long)st[2]);
     if (vec16 && !aligned16(ptr)) return fail(FA2_ERR_MISALIGNED, "%s is not 16-byte aligned", name);
     if (!vec16 && (reinterpret_cast<uintptr_t>(ptr) & 3u))
         return fail(FA2_ERR_MISALIGNED, "%s is not 4-byte aligned", name);

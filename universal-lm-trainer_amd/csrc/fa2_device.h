@@ -45,6 +45,10 @@ __device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
 // body into selects that would then run on every tile.
 #define FA2_COLD_BRANCH() asm volatile("" ::: "memory")
 
+// Kernel-local lambdas are always inlined: an out-of-line call would pass the
+// register arrays they work on through scratch memory.
+#define FA2_INLINE __attribute__((always_inline))
+
 // First MFMA of an accumulation chain: C is the constant zero.
 __device__ __forceinline__ f16x mfma32_first(h8 a, h8 b) {
     const f16x z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -107,6 +111,95 @@ __device__ __forceinline__ h8 tr_read8(const _Float16 *tile, int k0, int n0) {
         (const __attribute__((address_space(3))) _Float16 *)tile;
     const s4v r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + row * LD + col));
     const s4v r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + (row + 8) * LD + col));
+    const s8v both = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(h8, both);
+}
+
+// ---------------------------------------------------------------------------
+// Swizzled 64 x 64 fp16 tiles for direct global->LDS loads.
+//
+// A tile is 512 chunks of 16 bytes (8 halves); logical chunk ch (0..7) of row
+// r sits at chunk position 8*r + (ch ^ f(r)).  The XOR pattern is chosen per
+// read pattern so that the reads of one LDS pass touch distinct banks (for 32
+// and for 64 four-byte banks):
+//   * swz_rows(r): 16-byte reads of consecutive rows at one logical chunk
+//     (MFMA operands whose lane index runs along the rows);
+//   * swz_tr(r)  : transposing 8-byte reads of 4 rows x 32 bytes per 16 lanes
+//     (ds_read_b64_tr_b16 operands).
+// Both depend on r & 15 only, so rows 16 apart differ by a constant offset.
+__device__ __forceinline__ int swz_rows(int r) { return (r ^ ((r >> 3) & 1)) & 7; }
+__device__ __forceinline__ int swz_tr(int r) { return ((2 * r) & 6) | ((r >> 2) & 1); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte global->LDS transfer per lane (global_load_lds_dwordx4): lane L
+// of the wave writes the 16 bytes at byte address base + off to LDS bytes
+// [dst + 16*L, +16).  `base` (a wave-uniform 64-bit address held in SGPRs)
+// and `dst` must be wave-uniform; `off` is the lane's 32-bit byte offset, so
+// a tile's per-lane offsets stay in registers while only the scalar base
+// moves from tile to tile.  Completion is tracked by vmcnt only, so the
+// reader waits with vm_wait<N>() and a workgroup barrier (lds_barrier()).
+// Written as inline assembly: the compiler cannot tell which LDS reads a
+// transfer may feed and would otherwise put a vmcnt(0) -- a full drain of the
+// prefetch pipeline -- in front of them.  M0 (the LDS base of the transfer)
+// is saved and restored around it, since the compiler reserves that register.
+__device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, void *dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)dst);
+    // (readfirstlane returns int: each half goes through uint32_t so that the
+    // low word is zero-extended, not sign-extended, into the 64-bit address.)
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(sb), "s"(lds));
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the release fence of __syncthreads(), whose
+// vmcnt(0) would also drain every prefetch still in flight.  Outstanding LDS
+// reads are drained first; global->LDS transfers are waited for explicitly
+// with vm_wait.  The "memory" clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Value barrier: the value is computed before this point and the compiler
+// cannot move its computation past it (an empty volatile asm that "modifies"
+// the registers).
+template <typename T>
+__device__ __forceinline__ void pin(T &x) {
+    asm volatile("" : "+v"(x));
+}
+
+// Transposing operand read from a swz_tr-swizzled 64-row tile: the result of
+// tr_read8<64>(tile, k0, n0) for the unswizzled tile.  `lane_off` (bytes) is
+// tr_lane_off(n0) for this lane; k0 must be a multiple of 8.
+__device__ __forceinline__ int tr_lane_off(int n0) {
+    const int L = threadIdx.x & 63;
+    const int G = L >> 4, s = L & 15;
+    const int row = 4 * (G >> 1) + (s >> 2);               // row within an 8-row group
+    const int col = n0 + 16 * (G & 1) + 4 * (s & 3);
+    return row * 128 + (((col >> 3) ^ swz_tr(row)) << 4) + 2 * (col & 7);
+}
+
+__device__ __forceinline__ h8 tr_read8_sw(const _Float16 *tile, int lane_off, int k0) {
+    const char *base = reinterpret_cast<const char *>(tile) + lane_off + k0 * 128;
+    const __attribute__((address_space(3))) char *t = (const __attribute__((address_space(3))) char *)base;
+    const s4v r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t));
+    const s4v r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + 8 * 128));
     const s8v both = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(h8, both);
 }

@@ -8,14 +8,19 @@
 // tiles, causal tiles past the diagonal skipped, the denominator summed from
 // the un-dropped P, O = acc / l with l == 0 -> 0, LSE in natural log.
 //
-// Work decomposition (one workgroup = 4 waves = 256 queries of one (b, h)):
-//   * each wave owns 64 queries as two 32-query blocks; their Q^T operands
-//     (16 x 32 fp16 per d-step) stay in registers for the whole kernel;
-//   * key tiles of 64 are staged row-major through LDS, double buffered: K
-//     feeds the A operand of S^T = K Q^T with 16-byte reads, V feeds the A
-//     operand of O^T = V^T P^T through transposing ds_read_b64_tr_b16 reads;
-//     the next tile's global loads are in flight while the current tile is
-//     computed, one barrier per tile;
+// Work decomposition (one workgroup = 4 waves = 128 queries of one (b, h)):
+//   * each wave owns 32 queries; their Q^T operands (16 x 32 fp16 per
+//     d-step) stay in registers for the whole kernel;
+//   * key tiles of 64 keys are moved global -> LDS by the waves' direct
+//     transfers (global_load_lds, no register staging; a scalar tile base
+//     plus fixed 32-bit lane offsets) into XOR-swizzled tiles, four stages
+//     deep (three resident, one in flight); K feeds the A operand of
+//     S^T = K Q^T with 16-byte reads, V feeds the A operand of O^T = V^T P^T
+//     through transposing ds_read_b64_tr_b16 reads, both free of LDS bank
+//     conflicts;
+//   * the tile loop is software pipelined: step t issues the P V MFMAs of
+//     tile t-1 and the score MFMAs of tile t+1 while the VALU forms P of
+//     tile t, in chunks that pair two MFMAs with four exponentials;
 //   * S^T accumulators give each lane one query and 32 keys, so the row max
 //     is a local max plus one cross-half exchange, the running sum l stays a
 //     per-lane partial until the epilogue, the O^T rescale is a per-lane
@@ -24,10 +29,9 @@
 //   * no per-tile row max: P is formed against a lazily updated reference
 //     max and an overflow check on its row sum (v_dot2_f32_f16 on the packed
 //     fp16 P) decides when the true max, the O/l rescale and a recompute are
-//     needed, which is almost never after the first tile -- so the O
-//     accumulators are touched by MFMAs only;
-//   * at most 256 registers per lane, so two waves share each SIMD and one
-//     wave's softmax overlaps the other's MFMAs;
+//     needed, which is almost never after the first tile;
+//   * at most 256 registers per lane, so two workgroups share each CU and
+//     one's barrier waits are covered by the other's work;
 //   * workgroups are issued heaviest first (last query blocks first) and all
 //     workgroups of one (b, h) share blockIdx % 8, i.e. one XCD and its L2.
 #include "fa2_device.h"
@@ -36,19 +40,23 @@
 namespace fa2 {
 namespace {
 
-constexpr int NW = 4;              // waves per workgroup
-constexpr int QB = 2;              // 32-query blocks per wave
-constexpr int KT = 64;             // keys per tile
-constexpr int QWG = NW * 32 * QB;  // queries per workgroup
-constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <= 2^15
-#ifndef FA2_FWD_SCHED
-#define FA2_FWD_SCHED 0
+#ifndef FA2_FWD_NW
+#define FA2_FWD_NW 4
 #endif
+constexpr int NW = FA2_FWD_NW;     // waves per workgroup (4 or 8)
+constexpr int TPW = 8 / NW;        // 1 KB tile transfers per wave and tensor
+constexpr int KT = 64;             // keys per tile
+constexpr int QWG = NW * 32;       // queries per workgroup
+#ifndef FA2_FWD_NST
+#define FA2_FWD_NST 4
+#endif
+constexpr int NST = FA2_FWD_NST;   // LDS stages of (K, V) tiles: 4 or 5
+constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <= 2^15
 
 template <bool CAUSAL, bool DROPOUT>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 sK[2][KT * LDR];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][KT * LDR];
+__global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
+    // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
+    __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
@@ -68,230 +76,348 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
     float *Lp = a.lse + b * a.lsb + h * a.lsh;
 
     const int q_wg0 = qblk * QWG;
-    const int qw0 = q_wg0 + wave * 32 * QB;
+    const int qw0 = q_wg0 + wave * 32;   // this wave's queries: qw0 .. qw0 + 31
+    const int q = qw0 + c;               // this lane's query
     const float scale2 = a.scale2;
-
-    // Q^T operands: lane holds query (qw0 + 32*qb + c), d = 16*st + 8*g2 + e.
-    h8 qf[QB][4];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const int q = qw0 + 32 * qb + c;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            h8 v = zero_h8();
-            if (q < S) v = *reinterpret_cast<const h8 *>(Qp + q * a.qss + 16 * st + 8 * g2);
-            qf[qb][st] = a.negate ? neg_h8(v) : v;
-        }
-    }
-
-    f16x o[QB][2];
-    float msc[QB], l[QB];   // reference max (log2 units) and per-lane partial row sum
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        o[qb][0] = zero16();
-        o[qb][1] = zero16();
-        msc[qb] = -INFINITY;
-        l[qb] = 0.f;
-    }
 
     const int kend = CAUSAL ? min(S, q_wg0 + QWG) : S;
     const int ntiles = (kend + KT - 1) / KT;
+    // Last key tile this wave computes (-1: none).  Every wave still joins
+    // every barrier and moves its share of every tile.
+    const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32, S) - 1) / KT : ntiles - 1;
 
-    // Cooperative tile loader: thread -> key pair (2*lp, 2*lp+1), d chunk lc.
-    const int lp = tid >> 3;
-    const int lc = (tid & 7) * 8;
-    h8 kr0, kr1, vr0, vr1;
-    auto gload = [&](int k0) {
-        const int r0 = k0 + 2 * lp, r1 = r0 + 1;
-        kr0 = zero_h8();
-        kr1 = zero_h8();
-        vr0 = zero_h8();
-        vr1 = zero_h8();
-        if (r0 < S) {
-            kr0 = *reinterpret_cast<const h8 *>(Kp + r0 * a.kss + lc);
-            vr0 = *reinterpret_cast<const h8 *>(Vp + r0 * a.vss + lc);
+    // Q^T operand of d-step st: lane holds Q[q][16*st + 8*g2 + e].  Rows past
+    // S load row S - 1 (unconditional loads stay in flight together); those
+    // lanes' results are never stored.  Loaded before the first tiles, so
+    // waiting for a tile also covers them.
+    h8 qf[4];
+    {
+        const _Float16 *qrow = Qp + (int64_t)min(q, S - 1) * a.qss + 8 * g2;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const h8 v = *reinterpret_cast<const h8 *>(qrow + 16 * st);
+            qf[st] = a.negate ? neg_h8(v) : v;
         }
-        if (r1 < S) {
-            kr1 = *reinterpret_cast<const h8 *>(Kp + r1 * a.kss + lc);
-            vr1 = *reinterpret_cast<const h8 *>(Vp + r1 * a.vss + lc);
-        }
-    };
-    auto lstore = [&](int buf) {
-        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp) * LDR + lc]) = kr0;
-        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp + 1) * LDR + lc]) = kr1;
-        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp) * LDR + lc]) = vr0;
-        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp + 1) * LDR + lc]) = vr1;
-    };
-
-    if (ntiles > 0) {
-        gload(0);
-        lstore(0);
     }
-    __syncthreads();
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
+    // Tile loader: the 512 16-byte chunks of a K (or V) tile are 8 transfers
+    // of 64 lanes; wave w moves transfers j = 2w, 2w+1 of both.  Lane L of
+    // transfer j lands at chunk position 64j + L = 8*row + (L & 7) with
+    // row = 8j + (L >> 3), so it fetches logical chunk (L & 7) ^ swz(row) of
+    // key row k0 + row.  The lane's byte offsets within a tile are fixed; only
+    // the last tile, whose rows past S are redirected to row S - 1 (any
+    // finite row: their scores are masked and their P is zero), needs them
+    // recomputed.
+    const int lrow = lane >> 3;
+    const int kch[2] = {(lane & 7) ^ swz_rows(lrow), (lane & 7) ^ swz_rows(lrow + 8)};
+    const int vch = (lane & 7) ^ swz_tr(lrow);
+    auto tile_offsets = [&](int k0, uint32_t(&ko)[2], uint32_t(&vo)[2]) FA2_INLINE {
+#pragma unroll
+        for (int i = 0; i < TPW; ++i) {
+            const int row = min(k0 + 8 * (TPW * wave + i) + lrow, S - 1) - k0;
+            ko[i] = (uint32_t)(row * (int)a.kss + 8 * kch[(TPW * wave + i) & 1]) * 2u;   // kss < 2^24 (host check)
+            vo[i] = (uint32_t)(row * (int)a.vss + 8 * vch) * 2u;
+        }
+    };
+    uint32_t koffg[2], voffg[2];
+    tile_offsets(0, koffg, voffg);
+    auto issue = [&](int t) FA2_INLINE {
         const int k0 = t * KT;
-        if (t + 1 < ntiles) gload(k0 + KT);
-
-        const bool active = (qw0 < S) && (!CAUSAL || k0 <= qw0 + 32 * QB - 1);
-        if (active) {
-            const _Float16 *tK = sK[buf];
-            const _Float16 *tV = sV[buf];
-
-            // S^T = K Q^T : s[qb][kb] rows = keys k0 + 32*kb + (8i+4g2+j), col = query.
-            f16x s[QB][2];
+        uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
+        if (k0 + KT > S) tile_offsets(k0, ko, vo);
+        const _Float16 *kb = Kp + (int64_t)k0 * a.kss;
+        const _Float16 *vb = Vp + (int64_t)k0 * a.vss;
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const h8 ka0 = *reinterpret_cast<const h8 *>(tK + c * LDR + 16 * st + 8 * g2);
-                const h8 ka1 = *reinterpret_cast<const h8 *>(tK + (32 + c) * LDR + 16 * st + 8 * g2);
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    if (st == 0) {  // C = inline constant 0: no register zeroing
-                        s[qb][0] = mfma32_first(ka0, qf[qb][st]);
-                        s[qb][1] = mfma32_first(ka1, qf[qb][st]);
-                    } else {
-                        s[qb][0] = mfma32(ka0, qf[qb][st], s[qb][0]);
-                        s[qb][1] = mfma32(ka1, qf[qb][st], s[qb][1]);
-                    }
-                }
-            }
-
-            // Tail keys (>= S) and the causal triangle -> -inf.
-            const bool need_mask = (k0 + KT > S) || (CAUSAL && k0 + KT - 1 > qw0);
-            if (need_mask) {
-                FA2_COLD_BRANCH();
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    const int q = qw0 + 32 * qb + c;
-                    const int lim = CAUSAL ? min(q, S - 1) : S - 1;
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                            if (key > lim) s[qb][kb][r] = -INFINITY;
-                        }
-                }
-            }
-
-            // Online softmax against a lazily updated reference max msc (log2
-            // units).  P = exp2(s*scale2 - msc) is formed straight away, without
-            // a row max: the lane's fp16 P values are summed (fp32, v_dot2), and
-            // a partial sum <= 2^15 proves no P overflowed fp16.  Only when a
-            // sum exceeds that (or is inf/NaN, as on the first tile where msc =
-            // -inf) does the cold path take the true row max, rescale O and l,
-            // and recompute P.  l and LSE use whatever msc is current, so the
-            // result is the exact online softmax; the reference max only bounds
-            // the magnitudes (P <= 2^15).
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) {
-                h8 pb[2][2];
-                float rs = 0.f;
-                const float sub = msc[qb];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        f8 x;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            x[e] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][8 * hh + e], scale2, -sub));
-                        pb[kb][hh] = __builtin_convertvector(x, h8);
-                        rs = sum_h8(pb[kb][hh], rs);
-                    }
-                if (__any(!(rs <= P_SUM_LIMIT))) {
-                    FA2_COLD_BRANCH();
-                    float mx = s[qb][0][0];
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
-                    mx = fmaxf(mx, xor32(mx));
-                    const float mnew = fmaxf(msc[qb], mx * scale2);
-                    // mnew == -inf: every key so far masked; alpha stays 1 with O, l = 0
-                    const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc[qb] - mnew);
-                    msc[qb] = mnew;
-                    l[qb] *= alpha;
-#pragma unroll
-                    for (int db = 0; db < 2; ++db)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
-                    const float sub2 = (mnew == -INFINITY) ? 0.f : mnew;
-                    rs = 0.f;
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh) {
-                            f8 x;
-#pragma unroll
-                            for (int e = 0; e < 8; ++e)
-                                x[e] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][8 * hh + e], scale2, -sub2));
-                            pb[kb][hh] = __builtin_convertvector(x, h8);
-                            rs = sum_h8(pb[kb][hh], rs);
-                        }
-                }
-                if (DROPOUT) {
-                    // l sums the un-dropped P; dropout then zeroes / rescales P.
-                    const int q = qw0 + 32 * qb + c;
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) {
-                                const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
-                                const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
-                                pb[kb][hh][e] = keep ? (_Float16)((float)pb[kb][hh][e] * a.inv_keep)
-                                                     : (_Float16)0.f;
-                            }
-                }
-                l[qb] += rs;
-                // O^T += V^T P^T, contracting 16 keys per step.
-#pragma unroll
-                for (int db = 0; db < 2; ++db)
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh) {
-                            const h8 va = tr_read8<LDR>(tV, 32 * kb + 16 * hh, 32 * db);
-                            o[qb][db] = mfma32(va, pb[kb][hh], o[qb][db]);
-                        }
-            }
-#if FA2_FWD_SCHED
-            // Interleave: the 16 PV MFMAs each followed by a slice of VALU work.
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
-            }
-#endif
+        for (int i = 0; i < TPW; ++i) {
+            const int j = TPW * wave + i;
+            lds_dma16(kb, ko[i], sKV[t % NST][0] + 64 * j);
+            lds_dma16(vb, vo[i], sKV[t % NST][1] + 64 * j);
         }
-
-        if (t + 1 < ntiles) lstore(buf ^ 1);
-        __syncthreads();
-    }
-
-    // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
+    };
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const float lt = l[qb] + xor32(l[qb]);
-        const int q = qw0 + 32 * qb + c;
-        if (q < S) {
-            const float inv = lt > 0.f ? 1.f / lt : 0.f;
-            _Float16 *orow = Op + q * a.oss;
+    for (int t = 0; t < NST - 1; ++t)
+        if (t < ntiles) issue(t);
+
+    f16x o[2] = {zero16(), zero16()};   // O^T, d blocks 0..31 and 32..63
+    float msc = -INFINITY;              // reference max (log2 units)
+    float l = 0.f;                      // per-lane partial row sum
+
+    // Per-lane LDS byte offsets of the operand reads.
+    //   K (A operand of S^T): row c (+32 for kb = 1), logical chunk 2*st + g2.
+    int koff[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) koff[st] = c * 128 + (((2 * st + g2) ^ swz_rows(c)) << 4);
+    //   V^T (A operand of O^T, transposing reads), d block db.
+    const int voff0 = tr_lane_off(0), voff1 = tr_lane_off(32);
+
+    auto kread = [&](int stage, int st, int kb) FA2_INLINE {
+        return *reinterpret_cast<const h8 *>(reinterpret_cast<const char *>(sKV[stage][0]) + koff[st] +
+                                              kb * 32 * 128);
+    };
+    auto vread = [&](int stage, int db, int kb, int hh) FA2_INLINE {
+        return tr_read8_sw(reinterpret_cast<const _Float16 *>(sKV[stage][1]), db ? voff1 : voff0,
+                           32 * kb + 16 * hh);
+    };
+    // S^T = K Q^T against the K tile in `stage`: s[kb] rows = keys
+    // 32*kb + (8i+4g2+j) of the tile, column = this lane's query.  The reads
+    // run one d-step ahead; the scheduling barriers keep the compiler from
+    // hoisting all of them, which would raise the kernel's register peak.
+    auto s_mm = [&](int stage, f16x(&s)[2]) FA2_INLINE {
+        h8 n0 = kread(stage, 0, 0), n1 = kread(stage, 0, 1);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const h8 f0 = n0, f1 = n1;
+            if (st < 3) {
+                n0 = kread(stage, st + 1, 0);
+                n1 = kread(stage, st + 1, 1);
+            }
+            if (st == 0) {   // C = inline constant 0
+                s[0] = mfma32_first(f0, qf[0]);
+                s[1] = mfma32_first(f1, qf[0]);
+            } else {
+                s[0] = mfma32(f0, qf[st], s[0]);
+                s[1] = mfma32(f1, qf[st], s[1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // O^T += V^T P^T over the V tile in `stage`, 16 keys per MFMA.
+    auto pv = [&](int stage, const h8(&pb)[2][2]) FA2_INLINE {
+        h8 n0 = vread(stage, 0, 0, 0), n1 = vread(stage, 1, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {   // (kb, hh) = (i >> 1, i & 1)
+            const h8 f0 = n0, f1 = n1;
+            if (i < 3) {
+                n0 = vread(stage, 0, (i + 1) >> 1, (i + 1) & 1);
+                n1 = vread(stage, 1, (i + 1) >> 1, (i + 1) & 1);
+            }
+            o[0] = mfma32(f0, pb[i >> 1][i & 1], o[0]);
+            o[1] = mfma32(f1, pb[i >> 1][i & 1], o[1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // Tail keys (>= S) and the causal triangle -> -inf.  key = k0 + 32*kb +
+    // 4*g2 + (8*(r>>2) + (r&3)) is visible iff key <= lim; compared as a
+    // constant against a per-lane bound, so no key index is materialised.
+    auto need_mask = [&](int k0) FA2_INLINE { return (k0 + KT > S) || (CAUSAL && k0 + KT - 1 > qw0); };
+    auto mask = [&](int k0, f16x(&s)[2]) FA2_INLINE {
+        const int lim = CAUSAL ? min(q, S - 1) : S - 1;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int bound = lim - k0 - 32 * kb - 4 * g2;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (8 * (r >> 2) + (r & 3) > bound) s[kb][r] = -INFINITY;
+        }
+    };
+    // Online softmax against a lazily updated reference max msc (log2 units).
+    // P = exp2(s*scale2 - msc) is formed straight away, without a row max:
+    // the lane's fp16 P values are summed (fp32, v_dot2), and a partial sum
+    // <= 2^15 proves no P overflowed fp16.  Only when a sum exceeds that (or
+    // is inf/NaN, as on the first tile where msc = -inf) does the cold path
+    // take the true row max, rescale O and l, and form P again.  l and LSE
+    // use whatever msc is current, so the result is the exact online softmax;
+    // the reference max only bounds the magnitudes (P <= 2^15).
+    auto p_form = [&](const f16x(&s)[2], float sub, h8(&pb)[2][2]) FA2_INLINE {
+        float rs = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                f8 x;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hh + e], scale2, -sub));
+                pb[kb][hh] = __builtin_convertvector(x, h8);
+                rs = sum_h8(pb[kb][hh], rs);
+            }
+        return rs;
+    };
+    // After P of tile k0 (K tile in `stage`) was formed with partial sum rs:
+    // the cold path (scores recomputed from the K tile, so no score register
+    // has to outlive P), dropout, and the running sum.
+    auto softmax_tail = [&](int k0, int stage, h8(&pb)[2][2], float rs) FA2_INLINE {
+        if (__any(!(rs <= P_SUM_LIMIT))) {
+            FA2_COLD_BRANCH();
+            f16x s[2];
+            s_mm(stage, s);
+            if (need_mask(k0)) mask(k0, s);
+            float mx = s[0][0];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+            mx = fmaxf(mx, xor32(mx));
+            const float mnew = fmaxf(msc, mx * scale2);
+            // mnew == -inf: every key so far masked; alpha stays 1 with O, l = 0
+            const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc - mnew);
+            msc = mnew;
+            l *= alpha;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    f4 x;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j] * inv;
-                    *reinterpret_cast<h4 *>(orow + 32 * db + 8 * i + 4 * g2) =
-                        __builtin_convertvector(x, h4);
-                }
-            if (g2 == 0) Lp[q] = (msc[qb] == -INFINITY) ? -INFINITY : (msc[qb] + log2f(lt)) * LN2;
+                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+            rs = p_form(s, (mnew == -INFINITY) ? 0.f : mnew, pb);
         }
+        if (DROPOUT) {
+            // l sums the un-dropped P; dropout then zeroes / rescales P.
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
+                        const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
+                        pb[kb][hh][e] = keep ? (_Float16)((float)pb[kb][hh][e] * a.inv_keep) : (_Float16)0.f;
+                    }
+        }
+        l += rs;
+    };
+    // Steady-state step: O^T += V^T P_prev^T from V stage sv, s_next = K Q^T
+    // from K stage sk, and P_cur = exp2(s_cur * scale2 - msc), returning the
+    // lane's partial sum of P_cur.  Eight chunks, each two MFMAs and four
+    // exponentials, separated by scheduling barriers, with the operand reads
+    // of chunk i+1 issued in chunk i.  The PV MFMAs come first, while the
+    // first half of s_cur is consumed, and the score MFMAs second, so s_next
+    // only occupies registers once P_prev and half of s_cur are dead.
+    auto step = [&](int sk, int sv, f16x(&s_next)[2], const h8(&p_prev)[2][2], const f16x(&s_cur)[2],
+                    h8(&p_cur)[2][2]) FA2_INLINE {
+        // chunk i < 4: PV for (kb, hh) = (i >> 1, i & 1), d blocks 0 and 1;
+        // chunk i >= 4: scores for d-step i - 4, key blocks 0 and 1.
+        h8 n0 = vread(sv, 0, 0, 0), n1 = vread(sv, 1, 0, 0);
+        float rs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const h8 f0 = n0, f1 = n1;
+            if (i < 3) {
+                n0 = vread(sv, 0, (i + 1) >> 1, (i + 1) & 1);
+                n1 = vread(sv, 1, (i + 1) >> 1, (i + 1) & 1);
+            } else if (i < 7) {
+                n0 = kread(sk, i - 3, 0);
+                n1 = kread(sk, i - 3, 1);
+            }
+            if (i < 4) {
+                o[0] = mfma32(f0, p_prev[i >> 1][i & 1], o[0]);
+                o[1] = mfma32(f1, p_prev[i >> 1][i & 1], o[1]);
+            } else if (i == 4) {
+                s_next[0] = mfma32_first(f0, qf[0]);
+                s_next[1] = mfma32_first(f1, qf[0]);
+            } else {
+                s_next[0] = mfma32(f0, qf[i - 4], s_next[0]);
+                s_next[1] = mfma32(f1, qf[i - 4], s_next[1]);
+            }
+            // elements 4i .. 4i+3 of s_cur: kb = i >> 2, hh = (i >> 1) & 1, e0 = 4 (i & 1)
+            const int kb2 = i >> 2, hh2 = (i >> 1) & 1, e0 = 4 * (i & 1);
+            f4 x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(s_cur[kb2][8 * hh2 + e0 + e], scale2, -msc));
+            const h4 ph = __builtin_convertvector(x, h4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p_cur[kb2][hh2][e0 + e] = ph[e];
+            const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+            rs = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 0, 1), one, rs, false);
+            rs = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 2, 3), one, rs, false);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return rs;
+    };
+
+    // Software pipeline over key tiles:
+    //   step t: PV(t-1) with V_{t-1} | S(t+1) = K_{t+1} Q^T | P(t) from S(t)
+    // then the cold path of P(t) (which may re-read K_t), then one barrier.
+    // Tiles t-1 .. t+1 are resident during step t and tiles t+2 .. t+NST-2
+    // are in flight.  The barrier after step t publishes tile t+2 and frees
+    // the stage of tile t-1 for tile t+NST-1.
+    static_assert(NST == 4 || NST == 5, "three resident tiles plus one or two in flight");
+    // Tiles 0 and 1 have landed once at most the transfers of tiles
+    // 2 .. NST-2 are pending (4 per tile and wave).
+    if (NST == 5 && ntiles >= 4) vm_wait<8>(); else if (ntiles >= 3) vm_wait<4>(); else vm_wait<0>();
+    lds_barrier();
+
+    f16x s0[2], s1[2];          // scores of even / odd tiles
+    h8 p0[2][2], p1[2][2];      // P of even / odd tiles
+    if (tlast >= 0) s_mm(0, s0);
+    // Tile t keeps its scores and P in (s0, p0) for even t and (s1, p1) for
+    // odd t.  The end of a tile: tile t+2 landed (tiles up to t+NST-2 are
+    // issued), the barrier, and tile t+NST-1 into the stage of tile t-1.
+    auto tile_end = [&](int t) FA2_INLINE {
+        if (NST == 5 && t + 3 < ntiles) vm_wait<4>(); else if (t + 2 < ntiles) vm_wait<0>();
+        lds_barrier();
+        if (t + NST - 1 < ntiles) issue(t + NST - 1);
+    };
+    // Steady state (1 <= t < tlast): no masking -- the tile is below this
+    // wave's diagonal and not the last one -- and every group present.
+    auto steady = [&](int t, f16x(&s_cur)[2], h8(&p_cur)[2][2], f16x(&s_nxt)[2], h8(&p_prv)[2][2]) FA2_INLINE {
+        const float rs = step((t + 1) % NST, (t + NST - 1) % NST, s_nxt, p_prv, s_cur, p_cur);
+        softmax_tail(t * KT, t % NST, p_cur, rs);
+        tile_end(t);
+    };
+    // First tile, this wave's last (diagonal / tail) tile, and the tiles after
+    // it, where the wave only drains PV and keeps moving its share of tiles.
+    auto general = [&](int t, f16x(&s_cur)[2], h8(&p_cur)[2][2], f16x(&s_nxt)[2], h8(&p_prv)[2][2]) FA2_INLINE {
+        const int k0 = t * KT;
+        if (t >= 1 && t - 1 <= tlast) pv((t + NST - 1) % NST, p_prv);
+        if (t <= tlast) {
+            if (need_mask(k0)) {
+                FA2_COLD_BRANCH();
+                mask(k0, s_cur);
+            }
+            // Serial order (rare path): each operand dies before the next
+            // group's results are born, which keeps the register peak low.
+            softmax_tail(k0, t % NST, p_cur, p_form(s_cur, msc, p_cur));
+            if (t + 1 <= tlast) s_mm((t + 1) % NST, s_nxt);
+            if (t == ntiles - 1) pv(t % NST, p_cur);   // nothing after it drains P(t)
+        }
+        tile_end(t);
+    };
+    // Separate loops keep the steady body free of the general path's code,
+    // and every call site has fixed array roles: a role chosen at run time
+    // would make the compiler select between whole register arrays.
+    if (ntiles > 0) general(0, s0, p0, s1, p1);
+    int t = 1;
+    for (; t + 1 < tlast; t += 2) {   // t odd, t + 1 even
+        steady(t, s1, p1, s0, p0);
+        steady(t + 1, s0, p0, s1, p1);
+    }
+    if (t < tlast) {                   // t odd
+        steady(t, s1, p1, s0, p0);
+        ++t;
+    }
+    if (t & 1) {
+        // Tile t's scores and the previous P move to the even roles, once.
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const f16x ts = s0[kb];
+            s0[kb] = s1[kb];
+            s1[kb] = ts;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const h8 tp = p0[kb][hh];
+                p0[kb][hh] = p1[kb][hh];
+                p1[kb][hh] = tp;
+            }
+        }
+    }
+    for (; t < ntiles; t += 2) {
+        general(t, s0, p0, s1, p1);
+        if (t + 1 < ntiles) general(t + 1, s1, p1, s0, p0);
+    }
+
+    // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
+    const float lt = l + xor32(l);
+    if (q < S) {
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        _Float16 *orow = Op + (int64_t)q * a.oss;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f4 x;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[j] = o[db][4 * i + j] * inv;
+                *reinterpret_cast<h4 *>(orow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(x, h4);
+            }
+        if (g2 == 0) Lp[q] = (msc == -INFINITY) ? -INFINITY : (msc + log2f(lt)) * LN2;
     }
 }
 
@@ -300,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdArgs a) {
 hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const int nqblk = (a.S + QWG - 1) / QWG;
     const dim3 grid((unsigned)(nqblk * a.B * a.H));
-    const dim3 block(256);
+    const dim3 block(NW * 64);
     if (causal) {
         if (dropout)
             hipLaunchKernelGGL((fwd_kernel<true, true>), grid, block, 0, st, a);
