@@ -69,13 +69,15 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
  *   - 7: split pass like the reference -- a dQ kernel that also writes delta,
  *     then the dK/dV kernel (no atomics, run-to-run identical);
  *   - 2: the dQ kernel (writes delta); 1: delta only; 4: dK/dV reading the
- *     delta an earlier call left in the workspace;
+ *     delta and scaled LSE an earlier call (mode 1 or 2) left in the
+ *     workspace;
  *   - 14 or 15 (bit 8 with dQ and dK/dV): fused backward -- delta and a
  *     cleared fp32 dQ accumulator, one dK/dV kernel that also adds dS K into
  *     the accumulator with fp32 atomics, then dQ = scale * accumulator.
  *     Slower on MI355X (the atomics are L2-throughput bound); kept selectable.
- * The workspace (fa2_bwd_workspace_bytes) holds delta[b,h,i] = sum_d O*dO in
- * fp32 and the fp32 dQ accumulator. */
+ * The workspace (fa2_bwd_workspace_bytes) holds delta[b,h,i] = sum_d O*dO and
+ * LSE[b,h,i] * log2(e) in fp32 (written by the dQ or delta step, read by the
+ * dK/dV step) and the fp32 dQ accumulator.  B*H*S must be below 2^30. */
 typedef struct fa2_bwd_params {
     const void *q, *k, *v, *o, *dout;   /* fp16 [B,H,S,64]                     */
     const float *lse;                   /* fp32 [B,H,S] from the forward       */
@@ -90,8 +92,9 @@ typedef struct fa2_bwd_params {
     int32_t causal;
 } fa2_bwd_params;
 
-/* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta (4*B*H*S bytes,
- * rounded up to 256) followed by the fp32 dQ accumulator (256*B*H*S bytes). */
+/* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta and scaled LSE
+ * (8*B*H*S bytes, rounded up to 256) followed by the fp32 dQ accumulator
+ * (256*B*H*S bytes). */
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S);
 
 int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,

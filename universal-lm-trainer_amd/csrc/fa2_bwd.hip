@@ -48,7 +48,10 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const BwdArgs a) {
     sum += __shfl_xor(sum, 1);
     sum += __shfl_xor(sum, 2);
     sum += __shfl_xor(sum, 4);
-    if (row < S && part == 0) a.delta[(int64_t)bh * S + row] = sum;
+    if (row < S && part == 0) {
+        a.delta[(int64_t)bh * S + row] = sum;
+        if (a.lse) a.lse2[(int64_t)bh * S + row] = a.lse[b * a.lsb + h * a.lsh + row] * LOG2E;
+    }
     if (a.dqacc && row < S) {  // fused backward: clear this row of the fp32 dQ accumulator
         f4 *z = reinterpret_cast<f4 *>(a.dqacc + ((int64_t)bh * S + row) * HD + 8 * part);
         const f4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -137,7 +140,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
         }
         dl[qb] = part + xor32(part);
         lse2[qb] = valid ? Lp[q] * LOG2E : INFINITY;
-        if (valid && g2 == 0) Dp[q] = dl[qb];
+        if (valid && g2 == 0) {
+            Dp[q] = dl[qb];
+            a.lse2[(int64_t)bh * S + q] = lse2[qb];   // for the dK/dV pass
+        }
     }
 
     f16x dq[DQ_QB][2];
@@ -559,6 +565,341 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// dK / dV pass, software pipelined (the default backward's second kernel)
+// ---------------------------------------------------------------------------
+constexpr int KP_NW = 4;
+constexpr int KP_QT = 32;             // queries per tile
+constexpr int KP_KWG = KP_NW * 32;    // keys per workgroup
+#ifndef FA2_KV_NST
+#define FA2_KV_NST 4
+#endif
+constexpr int KP_NST = FA2_KV_NST;    // LDS stages: tiles t-1, t, t+1 resident, t+2 .. in flight (4..6)
+static_assert(KP_NST >= 4 && KP_NST <= 6, "dK/dV stages");
+
+// A workgroup owns 128 keys (32 per wave; K^T and V^T stay in registers) and
+// streams 32-query tiles: Q and dO by direct global->LDS transfers into
+// tiles swizzled so that both their row reads (S = Q K^T, dP = dO V^T) and
+// their transposed reads (dV += dO^T P, dK += Q^T dS) are free of bank
+// conflicts, and the tile's log2-scaled LSE and delta by one 4-byte transfer.
+// Step t issues the dK/dV MFMAs of tile t-1 and the S/dP MFMAs of tile t+1
+// while the VALU forms P and dS of tile t (reference @ None:
+// csrc/flash_attn_v100/flash_attn_v100_bwd.cu:300-470 computes the same
+// quantities per key tile).
+template <bool CAUSAL, bool DROPOUT>
+__global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) h8 sQD[KP_NST][2][KP_QT * 8];   // Q, dO tiles (4 KB each)
+    __shared__ __attribute__((aligned(16))) float sLD[KP_NST][2 * KP_QT];   // lse2[32], delta[32]
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, c = lane & 31, g2 = lane >> 5;
+    const int S = a.S;
+    const int BH = a.B * a.H;
+    const int L = blockIdx.x;
+    const int kblk = L / BH;              // key block 0 first: the heaviest under the causal mask
+    const int bh = L - kblk * BH;
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    const _Float16 *Qp = a.q + b * a.qsb + h * a.qsh;
+    const _Float16 *Kp = a.k + b * a.ksb + h * a.ksh;
+    const _Float16 *Vp = a.v + b * a.vsb + h * a.vsh;
+    const _Float16 *dOp = a.dout + b * a.dosb + h * a.dosh;
+    _Float16 *dKp = a.dk + b * a.dksb + h * a.dksh;
+    _Float16 *dVp = a.dv + b * a.dvsb + h * a.dvsh;
+
+    const int k_wg0 = kblk * KP_KWG;
+    const int kw0 = k_wg0 + 32 * wave;    // this wave's keys kw0 .. kw0 + 31
+    const int key = kw0 + c;               // this lane's key
+    const float scale2 = a.scale2;
+
+    // K^T / V^T B operands of d-step st: lane holds K[key][16*st + 8*g2 + e].
+    // Keys past S read row S - 1; their dK/dV columns are never stored.
+    h8 kf[4], vf[4];
+    {
+        const int kr = min(key, S - 1);
+        const _Float16 *krow = Kp + (int64_t)kr * a.kss + 8 * g2;
+        const _Float16 *vrow = Vp + (int64_t)kr * a.vss + 8 * g2;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const h8 kv = *reinterpret_cast<const h8 *>(krow + 16 * st);
+            kf[st] = a.negate ? neg_h8(kv) : kv;
+            vf[st] = *reinterpret_cast<const h8 *>(vrow + 16 * st);
+        }
+    }
+
+    const int q_start = CAUSAL ? k_wg0 : 0;
+    const int ntiles = (k_wg0 < S) ? (S - q_start + KP_QT - 1) / KP_QT : 0;
+    // First tile this wave computes (ntiles: none).  Causal: the tile holding
+    // the wave's diagonal; earlier tiles lie entirely above it.
+    const int tfirst = (kw0 >= S) ? ntiles : CAUSAL ? (kw0 - q_start) / KP_QT : 0;
+
+    // Tile loader.  Q and dO tiles are 256 chunks = 4 transfers each; wave w
+    // moves transfer w of both: lane L lands at chunk position 64w + L =
+    // 8*row + (L & 7), row = 8w + (L >> 3), and fetches logical chunk
+    // (L & 7) ^ swz_both(row) of query row q0 + row (rows past S: row S - 1,
+    // masked on use).  Wave 0 also moves the tile's lse2 (lanes 0..31) and
+    // delta (lanes 32..63) from the workspace, where lse2 = delta + B*H*S.
+    const int trow = 8 * wave + (lane >> 3);
+    const int tch = (lane & 7) ^ swz_both(trow);
+    auto tile_offsets = [&](int q0, uint32_t &qo, uint32_t &doo) FA2_INLINE {
+        const int row = min(q0 + trow, S - 1) - q0;
+        qo = (uint32_t)(row * (int)a.qss + 8 * tch) * 2u;     // strides < 2^24 (host check)
+        doo = (uint32_t)(row * (int)a.doss + 8 * tch) * 2u;
+    };
+    uint32_t qoff0, dooff0;
+    tile_offsets(0, qoff0, dooff0);
+    const uint32_t ldoff = ((lane < 32) ? (uint32_t)BH * (uint32_t)S * 4u : 0u) + 4u * (uint32_t)(lane & 31);
+    const float *ldbase = a.delta + (int64_t)bh * S;
+    auto issue = [&](int t) FA2_INLINE {
+        const int q0 = q_start + t * KP_QT;
+        uint32_t qo = qoff0, doo = dooff0;
+        if (q0 + KP_QT > S) tile_offsets(q0, qo, doo);
+        lds_dma16(Qp + (int64_t)q0 * a.qss, qo, sQD[t % KP_NST][0] + 64 * wave);
+        lds_dma16(dOp + (int64_t)q0 * a.doss, doo, sQD[t % KP_NST][1] + 64 * wave);
+        if (wave == 0) lds_dma4(ldbase + q0, ldoff, sLD[t % KP_NST]);
+    };
+#pragma unroll
+    for (int t = 0; t < KP_NST - 1; ++t)
+        if (t < ntiles) issue(t);
+    // Transfers per tile and wave: 2, plus 1 for wave 0.  Wait until at most
+    // n tiles' transfers are pending.
+    auto wait_tiles = [&](int n) FA2_INLINE {
+        if (n <= 0) vm_wait<0>();
+        else if (n == 1) { if (wave == 0) vm_wait<3>(); else vm_wait<2>(); }
+        else if (n == 2) { if (wave == 0) vm_wait<6>(); else vm_wait<4>(); }
+        else { if (wave == 0) vm_wait<9>(); else vm_wait<6>(); }
+    };
+    auto tile_end = [&](int t) FA2_INLINE {
+        // tile t+2 landed (tiles up to t+NST-2 issued); stage of tile t-1 free
+        wait_tiles(min(KP_NST - 4, ntiles - 1 - (t + 2)));
+        lds_barrier();
+        if (t + KP_NST - 1 < ntiles) issue(t + KP_NST - 1);
+    };
+
+    f16x dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};   // dK^T, dV^T (d blocks)
+
+    // LDS read offsets.  Row reads (A operands of S and dP): query row c,
+    // logical chunk 2*st + g2.  Transposed reads: d block db, row half hi.
+    int roff[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) roff[st] = c * 128 + (((2 * st + g2) ^ swz_both(c)) << 4);
+    int toff[2][2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) toff[db][hi] = tr_both_off(32 * db, hi);
+    auto rread = [&](int stage, int which, int st) FA2_INLINE {
+        return *reinterpret_cast<const h8 *>(reinterpret_cast<const char *>(sQD[stage][which]) + roff[st]);
+    };
+    auto tread = [&](int stage, int which, int db, int hh) FA2_INLINE {
+        return tr_read8_both(reinterpret_cast<const _Float16 *>(sQD[stage][which]), toff[db][0], toff[db][1],
+                             16 * hh);
+    };
+
+    // S = Q K^T and dP = dO V^T of the tile in `stage`: rows = the tile's
+    // queries 8i + 4*g2 + j, column = this lane's key.
+    auto sdp = [&](int stage, f16x &s, f16x &dp) FA2_INLINE {
+        h8 nq = rread(stage, 0, 0), nd = rread(stage, 1, 0);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const h8 fq = nq, fd = nd;
+            if (st < 3) {
+                nq = rread(stage, 0, st + 1);
+                nd = rread(stage, 1, st + 1);
+            }
+            if (st == 0) {
+                s = mfma32_first(fq, kf[0]);
+                dp = mfma32_first(fd, vf[0]);
+            } else {
+                s = mfma32(fq, kf[st], s);
+                dp = mfma32(fd, vf[st], dp);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // dV^T += dO^T P and dK^T += Q^T dS over the tile in `stage`.
+    auto dkdv = [&](int stage, const h8(&pb)[2], const h8(&dsb)[2]) FA2_INLINE {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {   // (db, hh) = (i >> 1, i & 1)
+            const int db = i >> 1, hh = i & 1;
+            dv[db] = mfma32(tread(stage, 1, db, hh), pb[hh], dv[db]);
+            dk[db] = mfma32(tread(stage, 0, db, hh), dsb[hh], dk[db]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // P and dS of element r (query row q) of a tile, from its score s, dP
+    // value g, lse2 l and delta dl.  Dropout: dV takes the kept, rescaled P;
+    // dS = P * (dP * keep / (1-p) - delta).
+    auto pds = [&](float sv, float g, float l, float dl, int q, float &pd, float &ds) FA2_INLINE {
+        const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -l));
+        if (DROPOUT) {
+            const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
+            pd = keep ? p * a.inv_keep : 0.f;
+            ds = pd * g - p * dl;
+        } else {
+            pd = p;
+            ds = p * (g - dl);
+        }
+    };
+    // The tile's lse2 / delta for this lane's rows 8i + 4*g2 + j.
+    auto stats = [&](int stage, f4(&l4)[4], f4(&d4)[4]) FA2_INLINE {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            l4[i] = *reinterpret_cast<const f4 *>(&sLD[stage][8 * i + 4 * g2]);
+            d4[i] = *reinterpret_cast<const f4 *>(&sLD[stage][KP_QT + 8 * i + 4 * g2]);
+        }
+    };
+    // General P / dS (first and last tiles): rows past S and, causal, keys
+    // after the query are forced to exactly zero (their lse2 / delta may be
+    // anything).
+    auto pds_general = [&](int t, const f16x &s, const f16x &dp, h8(&pb)[2], h8(&dsb)[2]) FA2_INLINE {
+        const int q0 = q_start + t * KP_QT;
+        f4 l4[4], d4[4];
+        stats(t % KP_NST, l4, d4);
+        const int lo = key - q0 - 4 * g2;        // visible iff off >= lo (causal)
+        const int hi = S - q0 - 4 * g2;          // and off < hi
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            f8 xp, xd;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int r = 8 * hh + e;
+                const int off = 8 * (r >> 2) + (r & 3);
+                float pd, ds;
+                pds(s[r], dp[r], l4[r >> 2][r & 3], d4[r >> 2][r & 3], q0 + 4 * g2 + off, pd, ds);
+                const bool vis = (!CAUSAL || off >= lo) && off < hi;
+                xp[e] = vis ? pd : 0.f;
+                xd[e] = vis ? ds : 0.f;
+            }
+            pb[hh] = __builtin_convertvector(xp, h8);
+            dsb[hh] = __builtin_convertvector(xd, h8);
+        }
+    };
+    // Steady step t (no masking: the tile is below the diagonal of every key
+    // of this wave and not the last one): dK/dV of tile t-1 from (pb_p,
+    // ds_p), S/dP of tile t+1 into (s_n, dp_n), P/dS of tile t from (s_c,
+    // dp_c) into (pb_c, ds_c).  Eight chunks of two MFMAs and two elements.
+    auto step_at = [&](int t, int sp, int sc_, int sn, f16x &s_n, f16x &dp_n, const h8(&pb_p)[2],
+                       const h8(&ds_p)[2], const f16x &s_c, const f16x &dp_c, h8(&pb_c)[2],
+                       h8(&ds_c)[2]) FA2_INLINE {
+        const int q0 = q_start + t * KP_QT;
+        f4 l4[4], d4[4];
+        stats(sc_, l4, d4);
+        // chunk i < 4: dK/dV for (db, hh) = (i >> 1, i & 1); i >= 4: S/dP for d-step i - 4
+        h8 n0 = tread(sp, 1, 0, 0), n1 = tread(sp, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const h8 f0 = n0, f1 = n1;
+            if (i < 3) {
+                n0 = tread(sp, 1, (i + 1) >> 1, (i + 1) & 1);
+                n1 = tread(sp, 0, (i + 1) >> 1, (i + 1) & 1);
+            } else if (i < 7) {
+                n0 = rread(sn, 0, i - 3);
+                n1 = rread(sn, 1, i - 3);
+            }
+            if (i < 4) {
+                const int db = i >> 1, hh = i & 1;
+                dv[db] = mfma32(f0, pb_p[hh], dv[db]);
+                dk[db] = mfma32(f1, ds_p[hh], dk[db]);
+            } else if (i == 4) {
+                s_n = mfma32_first(f0, kf[0]);
+                dp_n = mfma32_first(f1, vf[0]);
+            } else {
+                s_n = mfma32(f0, kf[i - 4], s_n);
+                dp_n = mfma32(f1, vf[i - 4], dp_n);
+            }
+            // elements r = 2i, 2i + 1 of tile t
+            f2 xp, xd;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int r = 2 * i + e;
+                float pd, ds;
+                pds(s_c[r], dp_c[r], l4[r >> 2][r & 3], d4[r >> 2][r & 3], q0 + 4 * g2 + 8 * (r >> 2) + (r & 3),
+                    pd, ds);
+                xp[e] = pd;
+                xd[e] = ds;
+            }
+            const h2 hp = __builtin_convertvector(xp, h2), hd = __builtin_convertvector(xd, h2);
+            pb_c[i >> 2][(2 * i) & 7] = hp[0];
+            pb_c[i >> 2][(2 * i + 1) & 7] = hp[1];
+            ds_c[i >> 2][(2 * i) & 7] = hd[0];
+            ds_c[i >> 2][(2 * i + 1) & 7] = hd[1];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto step = [&](int t, f16x &s_n, f16x &dp_n, const h8(&pb_p)[2], const h8(&ds_p)[2], const f16x &s_c,
+                    const f16x &dp_c, h8(&pb_c)[2], h8(&ds_c)[2]) FA2_INLINE {
+        step_at(t, (t + KP_NST - 1) % KP_NST, t % KP_NST, (t + 1) % KP_NST, s_n, dp_n, pb_p, ds_p, s_c, dp_c,
+                pb_c, ds_c);
+    };
+
+    // Tile t keeps its S, dP, P, dS in role X = (t - tfirst) & 1.
+    f16x sA, dpA, sB, dpB;
+    h8 pbA[2], dsA[2], pbB[2], dsB[2];
+    const int tl = ntiles - 1;
+    // Initial wait: tiles 0 and 1 landed, tiles 2 .. NST-2 may be in flight.
+    wait_tiles(min(KP_NST - 3, ntiles - 2));
+    lds_barrier();
+    for (int t = 0; t < min(tfirst, ntiles); ++t) tile_end(t);
+    if (tfirst < ntiles) {
+        // First tile: serial order, masked.
+        const int t0 = tfirst;
+        sdp(t0 % KP_NST, sA, dpA);
+        pds_general(t0, sA, dpA, pbA, dsA);
+        if (t0 + 1 < ntiles) sdp((t0 + 1) % KP_NST, sB, dpB);
+        if (t0 == tl) dkdv(t0 % KP_NST, pbA, dsA);
+        tile_end(t0);
+        int t = t0 + 1;
+        for (; t + 1 < tl; t += 2) {   // roles B (t) and A (t + 1)
+            step(t, sA, dpA, pbA, dsA, sB, dpB, pbB, dsB);
+            tile_end(t);
+            step(t + 1, sB, dpB, pbB, dsB, sA, dpA, pbA, dsA);
+            tile_end(t + 1);
+        }
+        if (t < tl) {                  // role B
+            step(t, sA, dpA, pbA, dsA, sB, dpB, pbB, dsB);
+            tile_end(t);
+            ++t;
+        }
+        if (t == tl && tl > t0) {
+            // Last tile: its S/dP sit in role (tl - t0) & 1; move them to A once.
+            if ((tl - t0) & 1) {
+                const f16x ts = sA, td = dpA;
+                sA = sB; dpA = dpB; sB = ts; dpB = td;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const h8 tp = pbA[hh], tq = dsA[hh];
+                    pbA[hh] = pbB[hh]; dsA[hh] = dsB[hh]; pbB[hh] = tp; dsB[hh] = tq;
+                }
+            }
+            dkdv((tl + KP_NST - 1) % KP_NST, pbB, dsB);   // tile tl - 1
+            pds_general(tl, sA, dpA, pbA, dsA);
+            dkdv(tl % KP_NST, pbA, dsA);
+            tile_end(tl);
+        }
+    }
+
+    const float sc = a.scale;
+    if (key < S) {
+        _Float16 *krow = dKp + (int64_t)key * a.dkss;
+        _Float16 *vrow = dVp + (int64_t)key * a.dvss;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f4 xk, xv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    xk[j] = dk[db][4 * i + j] * sc;
+                    xv[j] = dv[db][4 * i + j];
+                }
+                *reinterpret_cast<h4 *>(krow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xk, h4);
+                *reinterpret_cast<h4 *>(vrow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xv, h4);
+            }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st) {
@@ -602,7 +943,19 @@ static void launch_dkv_t(const BwdArgs &a, bool causal, bool dropout, hipStream_
 }
 
 hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
-    launch_dkv_t<false>(a, causal, dropout, st);
+    const int nkblk = (a.S + KP_KWG - 1) / KP_KWG;
+    const dim3 grid((unsigned)(nkblk * a.B * a.H)), block(256);
+    if (causal) {
+        if (dropout)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false>), grid, block, 0, st, a);
+    } else {
+        if (dropout)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false>), grid, block, 0, st, a);
+    }
     return hipGetLastError();
 }
 

@@ -133,8 +133,9 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
 
 // Workspace: fp32 delta [B*H*S] (rounded up to 256 bytes), then the fp32 dQ
 // accumulator [B*H*S*64] of the fused backward.
+// fp32 delta and log2-scaled LSE, [B*H*S] each, rounded up to 256 bytes.
 static size_t delta_bytes(int32_t B, int32_t H, int32_t S) {
-    return ((size_t)B * H * S * sizeof(float) + 255) & ~(size_t)255;
+    return ((size_t)B * H * S * 2 * sizeof(float) + 255) & ~(size_t)255;
 }
 
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S) {
@@ -150,6 +151,9 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     if (rc) return rc;
     if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
     if ((int64_t)p->B * p->H * p->S == 0 || mode == 0) return FA2_OK;
+    // The dK/dV pass reaches the LSE copy with a 32-bit byte offset from delta.
+    if ((int64_t)p->B * p->H * p->S >= (int64_t)1 << 30)
+        return fail(FA2_ERR_BAD_SHAPE, "B*H*S = %lld is not below 2^30", (long long)p->B * p->H * p->S);
     const size_t need = fa2_bwd_workspace_bytes(p->B, p->H, p->S);
     if (!workspace || workspace_bytes < need)
         return fail(FA2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : 0);
@@ -189,6 +193,7 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     a.dk = static_cast<_Float16 *>(p->dk);
     a.dv = static_cast<_Float16 *>(p->dv);
     a.delta = static_cast<float *>(workspace);
+    a.lse2 = a.delta + (int64_t)p->B * p->H * p->S;
     a.dqacc = fused ? reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S))
                     : nullptr;
     a.qsb = p->q_stride[0]; a.qsh = p->q_stride[1]; a.qss = p->q_stride[2];

@@ -25,6 +25,7 @@ namespace fa2 {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f8 __attribute__((ext_vector_type(8)));
 typedef float f16x __attribute__((ext_vector_type(16)));
@@ -126,9 +127,12 @@ __device__ __forceinline__ h8 tr_read8(const _Float16 *tile, int k0, int n0) {
 //     (MFMA operands whose lane index runs along the rows);
 //   * swz_tr(r)  : transposing 8-byte reads of 4 rows x 32 bytes per 16 lanes
 //     (ds_read_b64_tr_b16 operands).
-// Both depend on r & 15 only, so rows 16 apart differ by a constant offset.
+// All depend on r & 15 only, so rows 16 apart differ by a constant offset.
+//   * swz_both(r): both of the above on the same tile (an operand read as
+//     rows by one MFMA and transposed by another).
 __device__ __forceinline__ int swz_rows(int r) { return (r ^ ((r >> 3) & 1)) & 7; }
 __device__ __forceinline__ int swz_tr(int r) { return ((2 * r) & 6) | ((r >> 2) & 1); }
+__device__ __forceinline__ int swz_both(int r) { return swz_tr(r) ^ (((r >> 3) & 1) << 1); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -156,6 +160,24 @@ __device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, void *
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
         "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(sb), "s"(lds));
+}
+
+// The 4-byte form (global_load_lds_dword): lane L writes 4 bytes to LDS
+// bytes [dst + 4*L, +4).
+__device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, void *dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)dst);
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dword %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(off), "s"(sb), "s"(lds));
@@ -200,6 +222,27 @@ __device__ __forceinline__ h8 tr_read8_sw(const _Float16 *tile, int lane_off, in
     const __attribute__((address_space(3))) char *t = (const __attribute__((address_space(3))) char *)base;
     const s4v r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t));
     const s4v r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + 8 * 128));
+    const s8v both = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(h8, both);
+}
+
+// The same read from a swz_both-swizzled tile.  Its swizzle also depends on
+// row bit 3, so the two 8-row halves of a 16-row step have their own lane
+// offsets: tr_both_off(n0, 0) for rows k0 .. k0+7, tr_both_off(n0, 1) for
+// rows k0+8 .. k0+15; k0 must be a multiple of 16.
+__device__ __forceinline__ int tr_both_off(int n0, int hi) {
+    const int L = threadIdx.x & 63;
+    const int G = L >> 4, s = L & 15;
+    const int row = 4 * (G >> 1) + (s >> 2) + 8 * hi;      // row within a 16-row group
+    const int col = n0 + 16 * (G & 1) + 4 * (s & 3);
+    return row * 128 + (((col >> 3) ^ swz_both(row)) << 4) + 2 * (col & 7);
+}
+
+__device__ __forceinline__ h8 tr_read8_both(const _Float16 *tile, int off_lo, int off_hi, int k0) {
+    const char *base = reinterpret_cast<const char *>(tile) + k0 * 128;
+    const __attribute__((address_space(3))) char *t = (const __attribute__((address_space(3))) char *)base;
+    const s4v r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + off_lo));
+    const s4v r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v *)(t + off_hi));
     const s8v both = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(h8, both);
 }

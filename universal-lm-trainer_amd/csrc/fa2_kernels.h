@@ -27,7 +27,8 @@ struct BwdArgs {
     const _Float16 *q, *k, *v, *o, *dout;
     const float *lse;
     _Float16 *dq, *dk, *dv;
-    float *delta;        // [B*H, S] fp32 workspace
+    float *delta;        // [B*H, S] fp32 workspace: delta = rowsum(dO * O)
+    float *lse2;         // [B*H, S] fp32 workspace: LSE * log2(e), right after delta
     float *dqacc;        // [B*H, S, 64] fp32 dQ accumulator of the fused backward (or null)
     int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss;
     int64_t osb, osh, oss, dosb, dosh, doss;
