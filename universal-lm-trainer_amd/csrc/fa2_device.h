@@ -1,6 +1,7 @@
 // fa2_device.h -- device-side building blocks shared by the gfx950 attention
-// kernels: vector types, the fp16 MFMA wrapper, the LDS row swizzle, the
-// dropout hash and small cross-lane helpers.
+// kernels: vector types, the fp16 MFMA wrapper, LDS tile swizzles and
+// transposing reads, direct global->LDS transfers, the dropout hash and small
+// cross-lane helpers.
 //
 // Register layouts of v_mfma_f32_32x32x16_f16 (wave64, lane = 32*g2 + c):
 //   A operand (32 x 16, half8): lane holds A[m = c][k = 8*g2 + e], e = 0..7
@@ -13,8 +14,8 @@
 // operand of the next MFMA without leaving registers: registers 8*hh .. 8*hh+7
 // of an accumulator hold rows 16*hh + 8*(e/4) + 4*g2 + (e%4), which is exactly
 // the k order of a 16-deep B operand.  The A operand read from LDS must then
-// present its k index in that order, which the LDS layouts below provide by
-// swapping bits 2 and 3 of the k index within each 16-group (kperm).
+// present its k index in that order, which the transposing LDS reads below
+// (ds_read_b64_tr_b16) deliver directly.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -68,22 +69,6 @@ __device__ __forceinline__ h8 zero_h8() {
 #pragma unroll
     for (int i = 0; i < 8; ++i) z[i] = (_Float16)0.f;
     return z;
-}
-
-// Position of logical index k inside its LDS row: bits 2 and 3 swapped, so
-// that the 8 k values one lane feeds to a 16-deep MFMA step are contiguous.
-__device__ __forceinline__ int kperm(int k) {
-    return (k & ~0xC) | ((k & 4) << 1) | ((k & 8) >> 1);
-}
-
-// Element offset of (row, col) in a transposed tile [64 rows][LDR] whose
-// columns are in kperm order: the 16-byte chunk index is XOR-swizzled with
-// (row >> 3) & 7.  Rows 8 apart otherwise alias on the same banks (the row
-// stride is 36 dwords), which made the 4-byte transposing stores 8-way bank
-// conflicts; the swizzle spreads them while the 16-byte operand reads (8
-// consecutive rows, one chunk) stay conflict-free.
-__device__ __forceinline__ int tpos(int row, int col) {
-    return row * LDR + ((((col >> 3) ^ (row >> 3)) & 7) << 3) + (col & 7);
 }
 
 // Transposing operand read (ds_read_b64_tr_b16).  From a row-major LDS tile
@@ -196,14 +181,6 @@ __device__ __forceinline__ void vm_wait() {
 // accesses across it.
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Value barrier: the value is computed before this point and the compiler
-// cannot move its computation past it (an empty volatile asm that "modifies"
-// the registers).
-template <typename T>
-__device__ __forceinline__ void pin(T &x) {
-    asm volatile("" : "+v"(x));
 }
 
 // Transposing operand read from a swz_tr-swizzled 64-row tile: the result of

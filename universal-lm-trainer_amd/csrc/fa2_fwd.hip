@@ -310,13 +310,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
             const int kb2 = i >> 2, hh2 = (i >> 1) & 1, e0 = 4 * (i & 1);
             f4 x;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // Pinned here, so this chunk's exponentials are not hoisted
-                // ahead of the step's MFMAs.
-                float sv = s_cur[kb2][8 * hh2 + e0 + e];
-                pin(sv);
-                x[e] = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -msc));
-            }
+            for (int e = 0; e < 4; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(s_cur[kb2][8 * hh2 + e0 + e], scale2, -msc));
             const h4 ph = __builtin_convertvector(x, h4);
 #pragma unroll
             for (int e = 0; e < 4; ++e) p_cur[kb2][hh2][e0 + e] = ph[e];
@@ -353,18 +347,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     };
     // Steady state (1 <= t < tlast): no masking -- the tile is below this
     // wave's diagonal and not the last one -- and every group present.
-    // The step is dispatched on the stage of tile t, so that every LDS address
-    // in it is a per-lane base plus an instruction offset.
     auto steady = [&](int t, f16x(&s_cur)[2], h8(&p_cur)[2][2], f16x(&s_nxt)[2], h8(&p_prv)[2][2]) FA2_INLINE {
-        float rs;
-        static_assert(NST == 4 || NST == 5, "stage dispatch");
-        switch (t % NST) {
-            case 0: rs = step(1, NST - 1, s_nxt, p_prv, s_cur, p_cur); break;
-            case 1: rs = step(2, 0, s_nxt, p_prv, s_cur, p_cur); break;
-            case 2: rs = step(3, 1, s_nxt, p_prv, s_cur, p_cur); break;
-            case 3: rs = step(4 % NST, 2, s_nxt, p_prv, s_cur, p_cur); break;
-            default: rs = step(0, 3, s_nxt, p_prv, s_cur, p_cur); break;
-        }
+        const float rs = step((t + 1) % NST, (t + NST - 1) % NST, s_nxt, p_prv, s_cur, p_cur);
         softmax_tail(t * KT, t % NST, p_cur, rs);
         tile_end(t);
     };
