@@ -86,15 +86,18 @@ __global__ __launch_bounds__(256) void bwd_dq_convert_kernel(const BwdArgs a) {
 constexpr int DQ_NW = 4;
 constexpr int DQ_QB = 2;                    // 32-query blocks per wave
 constexpr int DQ_KT = 64;                   // keys per tile
+constexpr int DQ_NST = 3;                   // LDS stages (tiles in flight + 1)
 constexpr int DQ_QWG = DQ_NW * 32 * DQ_QB;  // 256 queries per workgroup
 
 template <bool CAUSAL, bool DROPOUT>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 sK[2][DQ_KT * LDR];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][DQ_KT * LDR];
+    // DQ_NST stages of a K and a V tile (8 KB each, swz_both chunks: K is
+    // read as rows for S^T and transposed for dQ^T, V as rows for dP^T).
+    __shared__ __attribute__((aligned(16))) h8 sKV[DQ_NST][2][DQ_KT * 8];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, c = lane & 31, g2 = lane >> 5;
     const int S = a.S;
     const int BH = a.B * a.H;
     const int nqblk = (S + DQ_QWG - 1) / DQ_QWG;
@@ -116,30 +119,30 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
     const int qw0 = q_wg0 + wave * 32 * DQ_QB;
     const float scale2 = a.scale2;
 
-    // Resident per-query operands and row statistics.
+    // Resident per-query operands and row statistics.  Rows past S read row
+    // S - 1 (unconditional loads stay in flight together) and get LSE = +inf,
+    // so their P and dS are zero.
     h8 qf[DQ_QB][4], dof[DQ_QB][4];
     float lse2[DQ_QB], dl[DQ_QB];
 #pragma unroll
     for (int qb = 0; qb < DQ_QB; ++qb) {
         const int q = qw0 + 32 * qb + c;
         const bool valid = q < S;
+        const int qr = min(q, S - 1);
         float part = 0.f;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            h8 qv = zero_h8(), dv = zero_h8(), ov = zero_h8();
-            if (valid) {
-                const int d0 = 16 * st + 8 * g2;
-                qv = *reinterpret_cast<const h8 *>(Qp + q * a.qss + d0);
-                dv = *reinterpret_cast<const h8 *>(dOp + q * a.doss + d0);
-                ov = *reinterpret_cast<const h8 *>(Op + q * a.oss + d0);
-            }
+            const int d0 = 16 * st + 8 * g2;
+            const h8 qv = *reinterpret_cast<const h8 *>(Qp + (int64_t)qr * a.qss + d0);
+            const h8 dv = *reinterpret_cast<const h8 *>(dOp + (int64_t)qr * a.doss + d0);
+            const h8 ov = *reinterpret_cast<const h8 *>(Op + (int64_t)qr * a.oss + d0);
             qf[qb][st] = a.negate ? neg_h8(qv) : qv;
             dof[qb][st] = dv;
 #pragma unroll
             for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)dv[e];
         }
         dl[qb] = part + xor32(part);
-        lse2[qb] = valid ? Lp[q] * LOG2E : INFINITY;
+        lse2[qb] = valid ? Lp[qr] * LOG2E : INFINITY;
         if (valid && g2 == 0) {
             Dp[q] = dl[qb];
             a.lse2[(int64_t)bh * S + q] = lse2[qb];   // for the dK/dV pass
@@ -156,64 +159,76 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
     const int kend = CAUSAL ? min(S, q_wg0 + DQ_QWG) : S;
     const int ntiles = (kend + DQ_KT - 1) / DQ_KT;
 
-    const int lp = tid >> 3;
-    const int lc = (tid & 7) * 8;
-    h8 kr0, kr1, vr0, vr1;
-    auto gload = [&](int k0) {
-        const int r0 = k0 + 2 * lp, r1 = r0 + 1;
-        kr0 = zero_h8();
-        kr1 = zero_h8();
-        vr0 = zero_h8();
-        vr1 = zero_h8();
-        if (r0 < S) {
-            kr0 = *reinterpret_cast<const h8 *>(Kp + r0 * a.kss + lc);
-            vr0 = *reinterpret_cast<const h8 *>(Vp + r0 * a.vss + lc);
-        }
-        if (r1 < S) {
-            kr1 = *reinterpret_cast<const h8 *>(Kp + r1 * a.kss + lc);
-            vr1 = *reinterpret_cast<const h8 *>(Vp + r1 * a.vss + lc);
+    // Tile loader (direct global->LDS transfers): wave w moves transfers
+    // j = 2w, 2w+1 of the K and the V tile; lane L of transfer j lands at chunk
+    // position 64j + L = 8*row + (L & 7), row = 8j + (L >> 3), and fetches
+    // logical chunk (L & 7) ^ swz_both(row) of key row k0 + row (rows past S:
+    // row S - 1, masked on use).
+    const int lrow = lane >> 3;
+    const int tch[2] = {(lane & 7) ^ swz_both(lrow), (lane & 7) ^ swz_both(lrow + 8)};
+    auto tile_offsets = [&](int k0, uint32_t(&ko)[2], uint32_t(&vo)[2]) FA2_INLINE {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = min(k0 + 8 * (2 * wave + i) + lrow, S - 1) - k0;
+            ko[i] = (uint32_t)(row * (int)a.kss + 8 * tch[i]) * 2u;   // strides < 2^24 (host check)
+            vo[i] = (uint32_t)(row * (int)a.vss + 8 * tch[i]) * 2u;
         }
     };
-    auto lstore = [&](int buf) {
-        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp) * LDR + lc]) = kr0;
-        *reinterpret_cast<h8 *>(&sK[buf][(2 * lp + 1) * LDR + lc]) = kr1;
-        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp) * LDR + lc]) = vr0;
-        *reinterpret_cast<h8 *>(&sV[buf][(2 * lp + 1) * LDR + lc]) = vr1;
+    uint32_t koffg[2], voffg[2];
+    tile_offsets(0, koffg, voffg);
+    auto issue = [&](int t) FA2_INLINE {
+        const int k0 = t * DQ_KT;
+        uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
+        if (k0 + DQ_KT > S) tile_offsets(k0, ko, vo);
+        const _Float16 *kb = Kp + (int64_t)k0 * a.kss;
+        const _Float16 *vb = Vp + (int64_t)k0 * a.vss;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            lds_dma16(kb, ko[i], sKV[t % DQ_NST][0] + 64 * (2 * wave + i));
+            lds_dma16(vb, vo[i], sKV[t % DQ_NST][1] + 64 * (2 * wave + i));
+        }
     };
+#pragma unroll
+    for (int t = 0; t < DQ_NST - 1; ++t)
+        if (t < ntiles) issue(t);
 
-    if (ntiles > 0) {
-        gload(0);
-        lstore(0);
-    }
-    __syncthreads();
+    // LDS read offsets: K / V rows 32*kb + c at logical chunk 2*st + g2, and
+    // K^T through transposing reads (d block db, row half hi).
+    int roff[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) roff[st] = c * 128 + (((2 * st + g2) ^ swz_both(c)) << 4);
+    int toff[2][2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) toff[db][hi] = tr_both_off(32 * db, hi);
 
     for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
         const int k0 = t * DQ_KT;
-        if (t + 1 < ntiles) gload(k0 + DQ_KT);
+        // Tile t landed once at most the transfers of the tiles issued after
+        // it (4 per tile and wave) are pending; the barrier publishes every
+        // wave's part and frees the stage of tile t - 1.
+        if (DQ_NST >= 3 && t + 1 < ntiles) vm_wait<4>(); else vm_wait<0>();
+        lds_barrier();
+        if (t + DQ_NST - 1 < ntiles) issue(t + DQ_NST - 1);
 
         const bool active = (qw0 < S) && (!CAUSAL || k0 <= qw0 + 32 * DQ_QB - 1);
         if (active) {
-            const _Float16 *tK = sK[buf];
-            const _Float16 *tV = sV[buf];
+            const char *tK = reinterpret_cast<const char *>(sKV[t % DQ_NST][0]);
+            const char *tV = reinterpret_cast<const char *>(sKV[t % DQ_NST][1]);
             const bool need_mask = (k0 + DQ_KT > S) || (CAUSAL && k0 + DQ_KT - 1 > qw0);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 // S^T = K Q^T and dP^T = V dO^T for 32 keys.
                 f16x s[DQ_QB], dp[DQ_QB];
 #pragma unroll
-                for (int qb = 0; qb < DQ_QB; ++qb) {
-                    s[qb] = zero16();
-                    dp[qb] = zero16();
-                }
-#pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const h8 ka = *reinterpret_cast<const h8 *>(tK + (32 * kb + c) * LDR + 16 * st + 8 * g2);
-                    const h8 va = *reinterpret_cast<const h8 *>(tV + (32 * kb + c) * LDR + 16 * st + 8 * g2);
+                    const h8 ka = *reinterpret_cast<const h8 *>(tK + roff[st] + kb * 32 * 128);
+                    const h8 va = *reinterpret_cast<const h8 *>(tV + roff[st] + kb * 32 * 128);
 #pragma unroll
                     for (int qb = 0; qb < DQ_QB; ++qb) {
-                        s[qb] = mfma32(ka, qf[qb][st], s[qb]);
-                        dp[qb] = mfma32(va, dof[qb][st], dp[qb]);
+                        s[qb] = st == 0 ? mfma32_first(ka, qf[qb][0]) : mfma32(ka, qf[qb][st], s[qb]);
+                        dp[qb] = st == 0 ? mfma32_first(va, dof[qb][0]) : mfma32(va, dof[qb][st], dp[qb]);
                     }
                 }
                 h8 dsb[DQ_QB][2];
@@ -221,13 +236,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
                 for (int qb = 0; qb < DQ_QB; ++qb) {
                     const int q = qw0 + 32 * qb + c;
                     if (need_mask) {
+                        // key = k0 + 32*kb + 4*g2 + (8*(r>>2) + (r&3)) visible iff key <= lim,
+                        // compared as a constant against a per-lane bound.
                         FA2_COLD_BRANCH();
-                        const int lim = CAUSAL ? min(q, S - 1) : S - 1;
+                        const int bound = (CAUSAL ? min(q, S - 1) : S - 1) - k0 - 32 * kb - 4 * g2;
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                            if (key > lim) s[qb][r] = -INFINITY;
-                        }
+                        for (int r = 0; r < 16; ++r)
+                            if (8 * (r >> 2) + (r & 3) > bound) s[qb][r] = -INFINITY;
                     }
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
@@ -247,15 +262,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        const h8 ka = tr_read8<LDR>(tK, 32 * kb + 16 * hh, 32 * db);
+                        const h8 ka = tr_read8_both(reinterpret_cast<const _Float16 *>(tK), toff[db][0], toff[db][1],
+                                                    32 * kb + 16 * hh);
 #pragma unroll
                         for (int qb = 0; qb < DQ_QB; ++qb) dq[qb][db] = mfma32(ka, dsb[qb][hh], dq[qb][db]);
                     }
             }
         }
-
-        if (t + 1 < ntiles) lstore(buf ^ 1);
-        __syncthreads();
     }
 
     const float sc = a.scale;
