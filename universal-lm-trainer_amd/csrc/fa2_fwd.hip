@@ -46,7 +46,11 @@ namespace {
 constexpr int NW = FA2_FWD_NW;     // waves per workgroup (4 or 8)
 constexpr int TPW = 8 / NW;        // 1 KB tile transfers per wave and tensor
 constexpr int KT = 64;             // keys per tile
-constexpr int QWG = NW * 32;       // queries per workgroup
+#ifndef FA2_FWD_QB
+#define FA2_FWD_QB 1
+#endif
+constexpr int QB = FA2_FWD_QB;     // 32-query blocks per wave (1: two waves per SIMD; 2: one)
+constexpr int QWG = NW * 32 * QB;  // queries per workgroup
 #ifndef FA2_FWD_NST
 #define FA2_FWD_NST 4
 #endif
@@ -54,7 +58,7 @@ constexpr int NST = FA2_FWD_NST;   // LDS stages of (K, V) tiles: 4 or 5
 constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <= 2^15
 
 template <bool CAUSAL, bool DROPOUT>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs a) {
     // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
     __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
 
@@ -76,27 +80,27 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     float *Lp = a.lse + b * a.lsb + h * a.lsh;
 
     const int q_wg0 = qblk * QWG;
-    const int qw0 = q_wg0 + wave * 32;   // this wave's queries: qw0 .. qw0 + 31
-    const int q = qw0 + c;               // this lane's query
+    const int qw0 = q_wg0 + wave * 32 * QB;   // this wave's queries: qw0 .. qw0 + 32*QB - 1
     const float scale2 = a.scale2;
 
     const int kend = CAUSAL ? min(S, q_wg0 + QWG) : S;
     const int ntiles = (kend + KT - 1) / KT;
     // Last key tile this wave computes (-1: none).  Every wave still joins
     // every barrier and moves its share of every tile.
-    const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32, S) - 1) / KT : ntiles - 1;
+    const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32 * QB, S) - 1) / KT : ntiles - 1;
 
     // Q^T operand of d-step st: lane holds Q[q][16*st + 8*g2 + e].  Rows past
     // S load row S - 1 (unconditional loads stay in flight together); those
     // lanes' results are never stored.  Loaded before the first tiles, so
     // waiting for a tile also covers them.
-    h8 qf[4];
-    {
-        const _Float16 *qrow = Qp + (int64_t)min(q, S - 1) * a.qss + 8 * g2;
+    h8 qf[QB][4];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const _Float16 *qrow = Qp + (int64_t)min(qw0 + 32 * qb + c, S - 1) * a.qss + 8 * g2;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             const h8 v = *reinterpret_cast<const h8 *>(qrow + 16 * st);
-            qf[st] = a.negate ? neg_h8(v) : v;
+            qf[qb][st] = a.negate ? neg_h8(v) : v;
         }
     }
 
@@ -138,9 +142,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     for (int t = 0; t < NST - 1; ++t)
         if (t < ntiles) issue(t);
 
-    f16x o[2] = {zero16(), zero16()};   // O^T, d blocks 0..31 and 32..63
-    float msc = -INFINITY;              // reference max (log2 units)
-    float l = 0.f;                      // per-lane partial row sum
+    f16x o[QB][2];                      // O^T, d blocks 0..31 and 32..63
+    float msc[QB], l[QB];               // reference max (log2 units), per-lane partial row sum
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        o[qb][0] = zero16();
+        o[qb][1] = zero16();
+        msc[qb] = -INFINITY;
+        l[qb] = 0.f;
+    }
 
     // Per-lane LDS byte offsets of the operand reads.
     //   K (A operand of S^T): row c (+32 for kb = 1), logical chunk 2*st + g2.
@@ -162,7 +172,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // 32*kb + (8i+4g2+j) of the tile, column = this lane's query.  The reads
     // run one d-step ahead; the scheduling barriers keep the compiler from
     // hoisting all of them, which would raise the kernel's register peak.
-    auto s_mm = [&](int stage, f16x(&s)[2]) FA2_INLINE {
+    auto s_mm = [&](int stage, f16x(&s)[QB][2]) FA2_INLINE {
         h8 n0 = kread(stage, 0, 0), n1 = kread(stage, 0, 1);
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
@@ -171,18 +181,21 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
                 n0 = kread(stage, st + 1, 0);
                 n1 = kread(stage, st + 1, 1);
             }
-            if (st == 0) {   // C = inline constant 0
-                s[0] = mfma32_first(f0, qf[0]);
-                s[1] = mfma32_first(f1, qf[0]);
-            } else {
-                s[0] = mfma32(f0, qf[st], s[0]);
-                s[1] = mfma32(f1, qf[st], s[1]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                if (st == 0) {   // C = inline constant 0
+                    s[qb][0] = mfma32_first(f0, qf[qb][0]);
+                    s[qb][1] = mfma32_first(f1, qf[qb][0]);
+                } else {
+                    s[qb][0] = mfma32(f0, qf[qb][st], s[qb][0]);
+                    s[qb][1] = mfma32(f1, qf[qb][st], s[qb][1]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
     // O^T += V^T P^T over the V tile in `stage`, 16 keys per MFMA.
-    auto pv = [&](int stage, const h8(&pb)[2][2]) FA2_INLINE {
+    auto pv = [&](int stage, const h8(&pb)[QB][2][2]) FA2_INLINE {
         h8 n0 = vread(stage, 0, 0, 0), n1 = vread(stage, 1, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {   // (kb, hh) = (i >> 1, i & 1)
@@ -191,8 +204,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
                 n0 = vread(stage, 0, (i + 1) >> 1, (i + 1) & 1);
                 n1 = vread(stage, 1, (i + 1) >> 1, (i + 1) & 1);
             }
-            o[0] = mfma32(f0, pb[i >> 1][i & 1], o[0]);
-            o[1] = mfma32(f1, pb[i >> 1][i & 1], o[1]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                o[qb][0] = mfma32(f0, pb[qb][i >> 1][i & 1], o[qb][0]);
+                o[qb][1] = mfma32(f1, pb[qb][i >> 1][i & 1], o[qb][1]);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -200,8 +216,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // 4*g2 + (8*(r>>2) + (r&3)) is visible iff key <= lim; compared as a
     // constant against a per-lane bound, so no key index is materialised.
     auto need_mask = [&](int k0) FA2_INLINE { return (k0 + KT > S) || (CAUSAL && k0 + KT - 1 > qw0); };
-    auto mask = [&](int k0, f16x(&s)[2]) FA2_INLINE {
-        const int lim = CAUSAL ? min(q, S - 1) : S - 1;
+    auto mask = [&](int qb, int k0, f16x(&s)[2]) FA2_INLINE {
+        const int lim = CAUSAL ? min(qw0 + 32 * qb + c, S - 1) : S - 1;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             const int bound = lim - k0 - 32 * kb - 4 * g2;
@@ -235,27 +251,28 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // After P of tile k0 (K tile in `stage`) was formed with partial sum rs:
     // the cold path (scores recomputed from the K tile, so no score register
     // has to outlive P), dropout, and the running sum.
-    auto softmax_tail = [&](int k0, int stage, h8(&pb)[2][2], float rs) FA2_INLINE {
+    auto softmax_tail = [&](int qb, int k0, int stage, h8(&pb)[2][2], float rs) FA2_INLINE {
         if (__any(!(rs <= P_SUM_LIMIT))) {
             FA2_COLD_BRANCH();
-            f16x s[2];
-            s_mm(stage, s);
-            if (need_mask(k0)) mask(k0, s);
+            f16x sq[QB][2];
+            s_mm(stage, sq);
+            f16x(&s)[2] = sq[qb];
+            if (need_mask(k0)) mask(qb, k0, s);
             float mx = s[0][0];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
             mx = fmaxf(mx, xor32(mx));
-            const float mnew = fmaxf(msc, mx * scale2);
+            const float mnew = fmaxf(msc[qb], mx * scale2);
             // mnew == -inf: every key so far masked; alpha stays 1 with O, l = 0
-            const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc - mnew);
-            msc = mnew;
-            l *= alpha;
+            const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc[qb] - mnew);
+            msc[qb] = mnew;
+            l[qb] *= alpha;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
             rs = p_form(s, (mnew == -INFINITY) ? 0.f : mnew, pb);
         }
         if (DROPOUT) {
@@ -267,11 +284,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
-                        const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
+                        const bool keep = dropout_keep(a.seed, qw0 + 32 * qb + c, key, (uint32_t)bh, a.drop_thr);
                         pb[kb][hh][e] = keep ? (_Float16)((float)pb[kb][hh][e] * a.inv_keep) : (_Float16)0.f;
                     }
         }
-        l += rs;
+        l[qb] += rs;
     };
     // Steady-state step: O^T += V^T P_prev^T from V stage sv, s_next = K Q^T
     // from K stage sk, and P_cur = exp2(s_cur * scale2 - msc), returning the
@@ -280,12 +297,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // of chunk i+1 issued in chunk i.  The PV MFMAs come first, while the
     // first half of s_cur is consumed, and the score MFMAs second, so s_next
     // only occupies registers once P_prev and half of s_cur are dead.
-    auto step = [&](int sk, int sv, f16x(&s_next)[2], const h8(&p_prev)[2][2], const f16x(&s_cur)[2],
-                    h8(&p_cur)[2][2]) FA2_INLINE {
+    auto step = [&](int sk, int sv, f16x(&s_next)[QB][2], const h8(&p_prev)[QB][2][2], const f16x(&s_cur)[QB][2],
+                    h8(&p_cur)[QB][2][2], float(&rs)[QB]) FA2_INLINE {
         // chunk i < 4: PV for (kb, hh) = (i >> 1, i & 1), d blocks 0 and 1;
-        // chunk i >= 4: scores for d-step i - 4, key blocks 0 and 1.
+        // chunk i >= 4: scores for d-step i - 4, key blocks 0 and 1; each for
+        // every query block, with the operand fragments shared.
         h8 n0 = vread(sv, 0, 0, 0), n1 = vread(sv, 1, 0, 0);
-        float rs = 0.f;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) rs[qb] = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const h8 f0 = n0, f1 = n1;
@@ -296,30 +315,33 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
                 n0 = kread(sk, i - 3, 0);
                 n1 = kread(sk, i - 3, 1);
             }
-            if (i < 4) {
-                o[0] = mfma32(f0, p_prev[i >> 1][i & 1], o[0]);
-                o[1] = mfma32(f1, p_prev[i >> 1][i & 1], o[1]);
-            } else if (i == 4) {
-                s_next[0] = mfma32_first(f0, qf[0]);
-                s_next[1] = mfma32_first(f1, qf[0]);
-            } else {
-                s_next[0] = mfma32(f0, qf[i - 4], s_next[0]);
-                s_next[1] = mfma32(f1, qf[i - 4], s_next[1]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                if (i < 4) {
+                    o[qb][0] = mfma32(f0, p_prev[qb][i >> 1][i & 1], o[qb][0]);
+                    o[qb][1] = mfma32(f1, p_prev[qb][i >> 1][i & 1], o[qb][1]);
+                } else if (i == 4) {
+                    s_next[qb][0] = mfma32_first(f0, qf[qb][0]);
+                    s_next[qb][1] = mfma32_first(f1, qf[qb][0]);
+                } else {
+                    s_next[qb][0] = mfma32(f0, qf[qb][i - 4], s_next[qb][0]);
+                    s_next[qb][1] = mfma32(f1, qf[qb][i - 4], s_next[qb][1]);
+                }
+                // elements 4i .. 4i+3 of s_cur: kb = i >> 2, hh = (i >> 1) & 1, e0 = 4 (i & 1)
+                const int kb2 = i >> 2, hh2 = (i >> 1) & 1, e0 = 4 * (i & 1);
+                f4 x;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    x[e] = __builtin_amdgcn_exp2f(fmaf(s_cur[qb][kb2][8 * hh2 + e0 + e], scale2, -msc[qb]));
+                const h4 ph = __builtin_convertvector(x, h4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p_cur[qb][kb2][hh2][e0 + e] = ph[e];
+                const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+                rs[qb] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 0, 1), one, rs[qb], false);
+                rs[qb] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 2, 3), one, rs[qb], false);
             }
-            // elements 4i .. 4i+3 of s_cur: kb = i >> 2, hh = (i >> 1) & 1, e0 = 4 (i & 1)
-            const int kb2 = i >> 2, hh2 = (i >> 1) & 1, e0 = 4 * (i & 1);
-            f4 x;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(s_cur[kb2][8 * hh2 + e0 + e], scale2, -msc));
-            const h4 ph = __builtin_convertvector(x, h4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p_cur[kb2][hh2][e0 + e] = ph[e];
-            const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-            rs = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 0, 1), one, rs, false);
-            rs = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 2, 3), one, rs, false);
             __builtin_amdgcn_sched_barrier(0);
         }
-        return rs;
     };
 
     // Software pipeline over key tiles:
@@ -334,8 +356,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     if (NST == 5 && ntiles >= 4) vm_wait<8>(); else if (ntiles >= 3) vm_wait<4>(); else vm_wait<0>();
     lds_barrier();
 
-    f16x s0[2], s1[2];          // scores of even / odd tiles
-    h8 p0[2][2], p1[2][2];      // P of even / odd tiles
+    f16x s0[QB][2], s1[QB][2];          // scores of even / odd tiles
+    h8 p0[QB][2][2], p1[QB][2][2];      // P of even / odd tiles
     if (tlast >= 0) s_mm(0, s0);
     // Tile t keeps its scores and P in (s0, p0) for even t and (s1, p1) for
     // odd t.  The end of a tile: tile t+2 landed (tiles up to t+NST-2 are
@@ -347,24 +369,31 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     };
     // Steady state (1 <= t < tlast): no masking -- the tile is below this
     // wave's diagonal and not the last one -- and every group present.
-    auto steady = [&](int t, f16x(&s_cur)[2], h8(&p_cur)[2][2], f16x(&s_nxt)[2], h8(&p_prv)[2][2]) FA2_INLINE {
-        const float rs = step((t + 1) % NST, (t + NST - 1) % NST, s_nxt, p_prv, s_cur, p_cur);
-        softmax_tail(t * KT, t % NST, p_cur, rs);
+    auto steady = [&](int t, f16x(&s_cur)[QB][2], h8(&p_cur)[QB][2][2], f16x(&s_nxt)[QB][2],
+                      h8(&p_prv)[QB][2][2]) FA2_INLINE {
+        float rs[QB];
+        step((t + 1) % NST, (t + NST - 1) % NST, s_nxt, p_prv, s_cur, p_cur, rs);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) softmax_tail(qb, t * KT, t % NST, p_cur[qb], rs[qb]);
         tile_end(t);
     };
     // First tile, this wave's last (diagonal / tail) tile, and the tiles after
     // it, where the wave only drains PV and keeps moving its share of tiles.
-    auto general = [&](int t, f16x(&s_cur)[2], h8(&p_cur)[2][2], f16x(&s_nxt)[2], h8(&p_prv)[2][2]) FA2_INLINE {
+    auto general = [&](int t, f16x(&s_cur)[QB][2], h8(&p_cur)[QB][2][2], f16x(&s_nxt)[QB][2],
+                       h8(&p_prv)[QB][2][2]) FA2_INLINE {
         const int k0 = t * KT;
         if (t >= 1 && t - 1 <= tlast) pv((t + NST - 1) % NST, p_prv);
         if (t <= tlast) {
-            if (need_mask(k0)) {
-                FA2_COLD_BRANCH();
-                mask(k0, s_cur);
-            }
             // Serial order (rare path): each operand dies before the next
             // group's results are born, which keeps the register peak low.
-            softmax_tail(k0, t % NST, p_cur, p_form(s_cur, msc, p_cur));
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                if (need_mask(k0)) {
+                    FA2_COLD_BRANCH();
+                    mask(qb, k0, s_cur[qb]);
+                }
+                softmax_tail(qb, k0, t % NST, p_cur[qb], p_form(s_cur[qb], msc[qb], p_cur[qb]));
+            }
             if (t + 1 <= tlast) s_mm((t + 1) % NST, s_nxt);
             if (t == ntiles - 1) pv(t % NST, p_cur);   // nothing after it drains P(t)
         }
@@ -386,17 +415,19 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     if (t & 1) {
         // Tile t's scores and the previous P move to the even roles, once.
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const f16x ts = s0[kb];
-            s0[kb] = s1[kb];
-            s1[kb] = ts;
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const h8 tp = p0[kb][hh];
-                p0[kb][hh] = p1[kb][hh];
-                p1[kb][hh] = tp;
+            for (int kb = 0; kb < 2; ++kb) {
+                const f16x ts = s0[qb][kb];
+                s0[qb][kb] = s1[qb][kb];
+                s1[qb][kb] = ts;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const h8 tp = p0[qb][kb][hh];
+                    p0[qb][kb][hh] = p1[qb][kb][hh];
+                    p1[qb][kb][hh] = tp;
+                }
             }
-        }
     }
     for (; t < ntiles; t += 2) {
         general(t, s0, p0, s1, p1);
@@ -404,20 +435,24 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     }
 
     // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
-    const float lt = l + xor32(l);
-    if (q < S) {
-        const float inv = lt > 0.f ? 1.f / lt : 0.f;
-        _Float16 *orow = Op + (int64_t)q * a.oss;
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
+    for (int qb = 0; qb < QB; ++qb) {
+        const float lt = l[qb] + xor32(l[qb]);
+        const int q = qw0 + 32 * qb + c;
+        if (q < S) {
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;
+            _Float16 *orow = Op + (int64_t)q * a.oss;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f4 x;
+            for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) x[j] = o[db][4 * i + j] * inv;
-                *reinterpret_cast<h4 *>(orow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(x, h4);
-            }
-        if (g2 == 0) Lp[q] = (msc == -INFINITY) ? -INFINITY : (msc + log2f(lt)) * LN2;
+                for (int i = 0; i < 4; ++i) {
+                    f4 x;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j] * inv;
+                    *reinterpret_cast<h4 *>(orow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(x, h4);
+                }
+            if (g2 == 0) Lp[q] = (msc[qb] == -INFINITY) ? -INFINITY : (msc[qb] + log2f(lt)) * LN2;
+        }
     }
 }
 
