@@ -39,8 +39,8 @@ HBM_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="2",
                     help="2, 3-512, 3-1024, 3-2048, 3-4096, 4, or 5 (10-layer decoder training step "
                          "with attention timed inside it)")
