@@ -834,6 +834,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                 xd[e] = ds;
             }
             const h2 hp = __builtin_convertvector(xp, h2), hd = __builtin_convertvector(xd, h2);
+            // Consumed here: keeps the chunk's VALU work beside its MFMAs
+            // (otherwise it is sunk past the tile's barrier to its use).
+            asm volatile("" ::"v"(hp), "v"(hd));
             pb_c[i >> 2][(2 * i) & 7] = hp[0];
             pb_c[i >> 2][(2 * i + 1) & 7] = hp[1];
             ds_c[i >> 2][(2 * i) & 7] = hd[0];
