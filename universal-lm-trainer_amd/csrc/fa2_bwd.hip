@@ -10,18 +10,19 @@
 //
 // dQ accumulation: split pass, like the reference (its dQ and dK/dV kernels,
 // bwd.cu:66-428), with no atomics:
-//   * bwd_dq_kernel : a workgroup owns 256 queries, keeps Q^T, dO^T, lse and
-//     delta of its queries in registers and streams key tiles (K, V row-major
-//     via LDS; K^T operands come from transposing ds_read_b64_tr_b16 reads).  It also computes delta itself (the reference's pre-pass,
+//   * bwd_dq_pipe_kernel: a workgroup owns 256 queries, keeps Q^T, dO^T, lse
+//     and delta of its queries in registers and streams key tiles (K, V
+//     row-major via LDS; K^T operands come from transposing ds_read_b64_tr_b16
+//     reads).  It also computes delta itself (the reference's pre-pass,
 //     bwd.cu:42-61) from the O and dO rows it holds and stores it for the
 //     dK/dV pass.  S^T and dP^T accumulators give each lane one query, so
 //     lse/delta are per-lane scalars and dS^T feeds the dQ^T = K^T dS^T MFMA
 //     straight from registers.
-//   * bwd_dkv_kernel: a workgroup owns 128 keys (32 per wave, K^T and V^T in
-//     registers), streams query tiles (Q, dO row-major, lse, delta via LDS;
-//     Q^T and dO^T operands through transposing reads) and accumulates dK^T
-//     and dV^T in registers; P and dS feed the dV/dK MFMAs straight from the
-//     S/dP accumulators.
+//   * bwd_dkv_pipe_kernel: a workgroup owns 128 keys (32 per wave, K^T and
+//     V^T in registers), streams query tiles (Q, dO row-major, lse, delta via
+//     LDS; Q^T and dO^T operands through transposing reads) and accumulates
+//     dK^T and dV^T in registers; P and dS feed the dV/dK MFMAs straight from
+//     the S/dP accumulators.  (bwd_dkv_kernel<FUSE> is the atomic-dQ variant.)
 #include "fa2_device.h"
 #include "fa2_kernels.h"
 
@@ -81,19 +82,25 @@ __global__ __launch_bounds__(256) void bwd_dq_convert_kernel(const BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ pass (+ delta)
+// dQ pass (+ delta), software pipelined
 // ---------------------------------------------------------------------------
 constexpr int DQ_NW = 4;
 constexpr int DQ_QB = 2;                    // 32-query blocks per wave
 constexpr int DQ_KT = 64;                   // keys per tile
-constexpr int DQ_NST = 3;                   // LDS stages (tiles in flight + 1)
 constexpr int DQ_QWG = DQ_NW * 32 * DQ_QB;  // 256 queries per workgroup
+constexpr int QP_NST = 4;   // LDS stages: key tiles t-1, t, t+1 resident, t+2 in flight
 
+// 256 queries per workgroup, 64 per wave, 64-key tiles, cut into units
+// u = 4t + 2kb + qb: key block kb (32 keys) of key tile t against query block
+// qb (32 queries) of the wave.  Step u issues the dQ MFMAs of unit u-1 and
+// the S/dP MFMAs of unit u+1 while the VALU forms dS of unit u, so the
+// exponentials and the dS arithmetic run beside matrix work of the same wave.
+// A unit reads its K / V fragments from LDS itself rather than sharing them
+// between the two query blocks, which keeps two units in flight within 256
+// registers.
 template <bool CAUSAL, bool DROPOUT>
-__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
-    // DQ_NST stages of a K and a V tile (8 KB each, swz_both chunks: K is
-    // read as rows for S^T and transposed for dQ^T, V as rows for dP^T).
-    __shared__ __attribute__((aligned(16))) h8 sKV[DQ_NST][2][DQ_KT * 8];
+__global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) h8 sKV[QP_NST][2][DQ_KT * 8];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -102,7 +109,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
     const int BH = a.B * a.H;
     const int nqblk = (S + DQ_QWG - 1) / DQ_QWG;
     const int L = blockIdx.x;
-    const int qblk = nqblk - 1 - L / BH;
+    const int qblk = nqblk - 1 - L / BH;   // heaviest (last) query blocks first
     const int bh = L - (L / BH) * BH;
     const int b = bh / a.H, h = bh - b * a.H;
 
@@ -119,9 +126,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
     const int qw0 = q_wg0 + wave * 32 * DQ_QB;
     const float scale2 = a.scale2;
 
-    // Resident per-query operands and row statistics.  Rows past S read row
-    // S - 1 (unconditional loads stay in flight together) and get LSE = +inf,
-    // so their P and dS are zero.
+    // Resident Q^T / dO^T operands, delta and log2-scaled LSE of the wave's
+    // queries (rows past S: row S - 1 and LSE = +inf, so P = dS = 0).
     h8 qf[DQ_QB][4], dof[DQ_QB][4];
     float lse2[DQ_QB], dl[DQ_QB];
 #pragma unroll
@@ -155,42 +161,66 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
         dq[qb][0] = zero16();
         dq[qb][1] = zero16();
     }
+    // Without dropout, dP^T - delta comes out of the MFMA chain: one extra
+    // bf16 step adds ones(k) * (-delta split into three bf16 parts, exact to
+    // fp32 rounding) over k = 0..2, so dS = P * acc needs no subtraction.
+    // Lanes of k half 1 (g2 = 1) hold zeros in both operands.
+    b8 dmb[DQ_QB], ones3;
+    if (!DROPOUT) {
+#pragma unroll
+        for (int qb = 0; qb < DQ_QB; ++qb) dmb[qb] = g2 == 0 ? split3_bf16(-dl[qb]) : zero_b8();
+        ones3 = g2 == 0 ? ones3_b8() : zero_b8();
+    }
 
     const int kend = CAUSAL ? min(S, q_wg0 + DQ_QWG) : S;
     const int ntiles = (kend + DQ_KT - 1) / DQ_KT;
+    // Last key tile of this wave (-1: none).  The wave's first query is a
+    // multiple of the tile size, so only that tile can need a mask.
+    const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32 * DQ_QB, S) - 1) / DQ_KT : ntiles - 1;
 
     // Tile loader (direct global->LDS transfers): wave w moves transfers
-    // j = 2w, 2w+1 of the K and the V tile; lane L of transfer j lands at chunk
-    // position 64j + L = 8*row + (L & 7), row = 8j + (L >> 3), and fetches
-    // logical chunk (L & 7) ^ swz_both(row) of key row k0 + row (rows past S:
-    // row S - 1, masked on use).
-    const int lrow = lane >> 3;
-    const int tch[2] = {(lane & 7) ^ swz_both(lrow), (lane & 7) ^ swz_both(lrow + 8)};
+    // j = 2w, 2w+1 of the K and the V tile; lane L of transfer j lands at
+    // chunk position 64j + L = 8*row + (L & 7), row = 8j + (L >> 3), and
+    // fetches logical chunk (L & 7) ^ swz_both(row) of key row k0 + row (rows
+    // past S: row S - 1, masked on use).
+    // Offsets are recomputed for every tile from the lane index, re-read
+    // through an opaque move so that nothing derived from it stays live
+    // across the tile loop: a few VALU operations per tile save registers.
     auto tile_offsets = [&](int k0, uint32_t(&ko)[2], uint32_t(&vo)[2]) FA2_INLINE {
+        int ln;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+        const int lrow = ln >> 3;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
+            const int ch = (ln & 7) ^ swz_both(lrow + 8 * i);
             const int row = min(k0 + 8 * (2 * wave + i) + lrow, S - 1) - k0;
-            ko[i] = (uint32_t)(row * (int)a.kss + 8 * tch[i]) * 2u;   // strides < 2^24 (host check)
-            vo[i] = (uint32_t)(row * (int)a.vss + 8 * tch[i]) * 2u;
+            ko[i] = (uint32_t)(row * (int)a.kss + 8 * ch) * 2u;   // strides < 2^24 (host check)
+            vo[i] = (uint32_t)(row * (int)a.vss + 8 * ch) * 2u;
         }
     };
-    uint32_t koffg[2], voffg[2];
-    tile_offsets(0, koffg, voffg);
     auto issue = [&](int t) FA2_INLINE {
         const int k0 = t * DQ_KT;
-        uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
-        if (k0 + DQ_KT > S) tile_offsets(k0, ko, vo);
+        uint32_t ko[2], vo[2];
+        tile_offsets(k0, ko, vo);
         const _Float16 *kb = Kp + (int64_t)k0 * a.kss;
         const _Float16 *vb = Vp + (int64_t)k0 * a.vss;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            lds_dma16(kb, ko[i], sKV[t % DQ_NST][0] + 64 * (2 * wave + i));
-            lds_dma16(vb, vo[i], sKV[t % DQ_NST][1] + 64 * (2 * wave + i));
+            lds_dma16(kb, ko[i], sKV[t % QP_NST][0] + 64 * (2 * wave + i));
+            lds_dma16(vb, vo[i], sKV[t % QP_NST][1] + 64 * (2 * wave + i));
         }
     };
 #pragma unroll
-    for (int t = 0; t < DQ_NST - 1; ++t)
+    for (int t = 0; t < QP_NST - 1; ++t)
         if (t < ntiles) issue(t);
+    // End of tile t's third step: tile t+1 landed (tiles up to t+2 are issued,
+    // 4 transfers per tile and wave), the barrier publishes it and frees the
+    // stage of tile t-1 (last read by step 4t), and tile t+3 goes into it.
+    auto tile_end = [&](int t) FA2_INLINE {
+        if (t + 2 < ntiles) vm_wait<4>(); else vm_wait<0>();
+        lds_barrier();
+        if (t + QP_NST - 1 < ntiles) issue(t + QP_NST - 1);
+    };
 
     // LDS read offsets: K / V rows 32*kb + c at logical chunk 2*st + g2, and
     // K^T through transposing reads (d block db, row half hi).
@@ -202,74 +232,154 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const BwdArgs a) {
     for (int db = 0; db < 2; ++db)
 #pragma unroll
         for (int hi = 0; hi < 2; ++hi) toff[db][hi] = tr_both_off(32 * db, hi);
+    auto rrow = [&](int stage, int which, int kb, int st) FA2_INLINE {
+        return *reinterpret_cast<const h8 *>(reinterpret_cast<const char *>(sKV[stage][which]) + roff[st] +
+                                             kb * 32 * 128);
+    };
+    auto trk = [&](int stage, int kb, int db, int hh) FA2_INLINE {
+        return tr_read8_both(reinterpret_cast<const _Float16 *>(sKV[stage][0]), toff[db][0], toff[db][1],
+                             32 * kb + 16 * hh);
+    };
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int k0 = t * DQ_KT;
-        // Tile t landed once at most the transfers of the tiles issued after
-        // it (4 per tile and wave) are pending; the barrier publishes every
-        // wave's part and frees the stage of tile t - 1.
-        if (DQ_NST >= 3 && t + 1 < ntiles) vm_wait<4>(); else vm_wait<0>();
-        lds_barrier();
-        if (t + DQ_NST - 1 < ntiles) issue(t + DQ_NST - 1);
-
-        const bool active = (qw0 < S) && (!CAUSAL || k0 <= qw0 + 32 * DQ_QB - 1);
-        if (active) {
-            const char *tK = reinterpret_cast<const char *>(sKV[t % DQ_NST][0]);
-            const char *tV = reinterpret_cast<const char *>(sKV[t % DQ_NST][1]);
-            const bool need_mask = (k0 + DQ_KT > S) || (CAUSAL && k0 + DQ_KT - 1 > qw0);
+    // S^T = K Q^T and dP^T = V dO^T of unit (stage, kb, qb).
+    auto sdp = [&](int stage, int kb, int qb, f16x &s, f16x &dp) FA2_INLINE {
+        if (!DROPOUT) dp = mfma32_bf16_first(ones3, dmb[qb]);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                // S^T = K Q^T and dP^T = V dO^T for 32 keys.
-                f16x s[DQ_QB], dp[DQ_QB];
-#pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const h8 ka = *reinterpret_cast<const h8 *>(tK + roff[st] + kb * 32 * 128);
-                    const h8 va = *reinterpret_cast<const h8 *>(tV + roff[st] + kb * 32 * 128);
-#pragma unroll
-                    for (int qb = 0; qb < DQ_QB; ++qb) {
-                        s[qb] = st == 0 ? mfma32_first(ka, qf[qb][0]) : mfma32(ka, qf[qb][st], s[qb]);
-                        dp[qb] = st == 0 ? mfma32_first(va, dof[qb][0]) : mfma32(va, dof[qb][st], dp[qb]);
-                    }
-                }
-                h8 dsb[DQ_QB][2];
-#pragma unroll
-                for (int qb = 0; qb < DQ_QB; ++qb) {
-                    const int q = qw0 + 32 * qb + c;
-                    if (need_mask) {
-                        // key = k0 + 32*kb + 4*g2 + (8*(r>>2) + (r&3)) visible iff key <= lim,
-                        // compared as a constant against a per-lane bound.
-                        FA2_COLD_BRANCH();
-                        const int bound = (CAUSAL ? min(q, S - 1) : S - 1) - k0 - 32 * kb - 4 * g2;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            if (8 * (r >> 2) + (r & 3) > bound) s[qb][r] = -INFINITY;
-                    }
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float p = __builtin_amdgcn_exp2f(fmaf(s[qb][r], scale2, -lse2[qb]));
-                        float g = dp[qb][r];
-                        if (DROPOUT) {
-                            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                            g = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr) ? g * a.inv_keep : 0.f;
-                        }
-                        s[qb][r] = p * (g - dl[qb]);
-                    }
-                    dsb[qb][0] = acc_to_h8(s[qb], 0);
-                    dsb[qb][1] = acc_to_h8(s[qb], 1);
-                }
-                // dQ^T += K^T dS^T over these 32 keys.
-#pragma unroll
-                for (int db = 0; db < 2; ++db)
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const h8 ka = tr_read8_both(reinterpret_cast<const _Float16 *>(tK), toff[db][0], toff[db][1],
-                                                    32 * kb + 16 * hh);
-#pragma unroll
-                        for (int qb = 0; qb < DQ_QB; ++qb) dq[qb][db] = mfma32(ka, dsb[qb][hh], dq[qb][db]);
-                    }
-            }
+        for (int st = 0; st < 4; ++st) {
+            const h8 ka = rrow(stage, 0, kb, st), va = rrow(stage, 1, kb, st);
+            s = st == 0 ? mfma32_first(ka, qf[qb][0]) : mfma32(ka, qf[qb][st], s);
+            dp = (st == 0 && DROPOUT) ? mfma32_first(va, dof[qb][0]) : mfma32(va, dof[qb][st], dp);
         }
+    };
+    // dQ^T += K^T dS^T of unit (stage, kb, qb).
+    auto dq_mm = [&](int stage, int kb, int qb, const h8(&dsb)[2]) FA2_INLINE {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < 2; ++db) dq[qb][db] = mfma32(trk(stage, kb, db, hh), dsb[hh], dq[qb][db]);
+    };
+    // Keys past S and, causal, after the query -> -inf.  key = t*KT + 32*kb +
+    // 4*g2 + (8*(r>>2) + (r&3)), compared as a constant against a per-lane bound.
+    auto need_mask = [&](int t) FA2_INLINE {
+        return (t * DQ_KT + DQ_KT > S) || (CAUSAL && t * DQ_KT + DQ_KT - 1 > qw0);
+    };
+    auto mask = [&](int t, int kb, int qb, f16x &s) FA2_INLINE {
+        const int q = qw0 + 32 * qb + c;
+        const int bound = (CAUSAL ? min(q, S - 1) : S - 1) - t * DQ_KT - 32 * kb - 4 * g2;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) > bound) s[r] = -INFINITY;
+    };
+    // dS of element r of unit (t, kb, qb) from its score and dP value.
+    // (Without dropout g is dP - delta already.)
+    auto ds_of = [&](float sv, float g, int t, int kb, int qb, int r) FA2_INLINE {
+        const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -lse2[qb]));
+        if (!DROPOUT) return p * g;
+        const int key = t * DQ_KT + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
+        g = dropout_keep(a.seed, qw0 + 32 * qb + c, key, (uint32_t)bh, a.drop_thr) ? g * a.inv_keep : 0.f;
+        return p * (g - dl[qb]);
+    };
+    auto ds_form = [&](int t, int kb, int qb, const f16x &s, const f16x &dp, h8(&dsb)[2]) FA2_INLINE {
+        f16x x;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = ds_of(s[r], dp[r], t, kb, qb, r);
+        dsb[0] = acc_to_h8(x, 0);
+        dsb[1] = acc_to_h8(x, 1);
+    };
+
+    // Pipelined step: dS of unit (t, kb, qb) from (s_c, dp_c) into ds_c; the
+    // dQ MFMAs of the previous unit (stage sp, kbp, qbp, from ds_p); the S/dP
+    // MFMAs of the next unit (stage sn, kbn, qbn) into (s_n, dp_n).  Six
+    // chunks of two MFMAs (dQ for hh = 0, 1, then S/dP for d-steps 0..3), the
+    // operand reads of chunk i+1 issued in chunk i, elements 3,3,3,3,2,2.
+    auto step = [&](int t, int kb, int qb, const f16x &s_c, const f16x &dp_c, h8(&ds_c)[2], int sp, int kbp,
+                    int qbp, const h8(&ds_p)[2], int sn, int kbn, int qbn, f16x &s_n, f16x &dp_n) FA2_INLINE {
+        h8 n0 = trk(sp, kbp, 0, 0), n1 = trk(sp, kbp, 1, 0);
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const h8 f0 = n0, f1 = n1;
+            if (i == 0) {
+                n0 = trk(sp, kbp, 0, 1);
+                n1 = trk(sp, kbp, 1, 1);
+            } else if (i < 5) {
+                n0 = rrow(sn, 0, kbn, i - 1);
+                n1 = rrow(sn, 1, kbn, i - 1);
+            }
+            if (i < 2) {
+                dq[qbp][0] = mfma32(f0, ds_p[i], dq[qbp][0]);
+                dq[qbp][1] = mfma32(f1, ds_p[i], dq[qbp][1]);
+                if (i == 1 && !DROPOUT) dp_n = mfma32_bf16_first(ones3, dmb[qbn]);
+            } else if (i == 2) {
+                s_n = mfma32_first(f0, qf[qbn][0]);
+                dp_n = DROPOUT ? mfma32_first(f1, dof[qbn][0]) : mfma32(f1, dof[qbn][0], dp_n);
+            } else {
+                s_n = mfma32(f0, qf[qbn][i - 2], s_n);
+                dp_n = mfma32(f1, dof[qbn][i - 2], dp_n);
+            }
+            const int elo = i < 4 ? 3 * i : 12 + 2 * (i - 4);
+            const int ehi = i < 3 ? 3 * i + 3 : 12 + 2 * (i - 3);
+#pragma unroll
+            for (int e = elo; e < ehi; ++e) {
+                x[e] = ds_of(s_c[e], dp_c[e], t, kb, qb, e);
+                if (e & 1) {
+                    const f2 xx = {x[e - 1], x[e]};
+                    const h2 hd = __builtin_convertvector(xx, h2);
+                    // Consumed here: keeps the chunk's VALU work beside its MFMAs.
+                    asm volatile("" ::"v"(hd));
+                    ds_c[e >> 3][(e - 1) & 7] = hd[0];
+                    ds_c[e >> 3][e & 7] = hd[1];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Query block qb's units keep S, dP and dS in role qb (A: 0, B: 1).
+    f16x sA, dpA, sB, dpB;
+    h8 dsA[2], dsB[2];
+    // Tile 0 landed once at most the transfers of tiles 1 and 2 are pending.
+    if (ntiles >= 3) vm_wait<8>(); else if (ntiles == 2) vm_wait<4>(); else vm_wait<0>();
+    lds_barrier();
+    if (tlast >= 0) {
+        sdp(0, 0, 0, sA, dpA);
+        dsB[0] = zero_h8();   // tile 0's first step adds K * 0 for the (absent) unit before it
+        dsB[1] = zero_h8();
+        int t = 0;
+        for (; t < tlast; ++t) {
+            const int st = t % QP_NST, sp = (t + QP_NST - 1) % QP_NST, sn = (t + 1) % QP_NST;
+            step(t, 0, 0, sA, dpA, dsA, t > 0 ? sp : st, 1, 1, dsB, st, 0, 1, sB, dpB);
+            step(t, 0, 1, sB, dpB, dsB, st, 0, 0, dsA, st, 1, 0, sA, dpA);
+            step(t, 1, 0, sA, dpA, dsA, st, 0, 1, dsB, st, 1, 1, sB, dpB);
+            tile_end(t);
+            step(t, 1, 1, sB, dpB, dsB, st, 1, 0, dsA, sn, 0, 0, sA, dpA);
+        }
+        // Tile tlast in serial order, masked where needed.
+        const int st = t % QP_NST, sp = (t + QP_NST - 1) % QP_NST;
+        const bool m = need_mask(t);
+        if (m) {
+            FA2_COLD_BRANCH();
+            mask(t, 0, 0, sA);
+        }
+        ds_form(t, 0, 0, sA, dpA, dsA);
+        if (t > 0) dq_mm(sp, 1, 1, dsB);
+        dq_mm(st, 0, 0, dsA);
+        sdp(st, 0, 1, sB, dpB);
+        if (m) mask(t, 0, 1, sB);
+        ds_form(t, 0, 1, sB, dpB, dsB);
+        dq_mm(st, 0, 1, dsB);
+        sdp(st, 1, 0, sA, dpA);
+        if (m) mask(t, 1, 0, sA);
+        ds_form(t, 1, 0, sA, dpA, dsA);
+        dq_mm(st, 1, 0, dsA);
+        sdp(st, 1, 1, sB, dpB);
+        if (m) mask(t, 1, 1, sB);
+        ds_form(t, 1, 1, sB, dpB, dsB);
+        dq_mm(st, 1, 1, dsB);
+        if (t < ntiles - 1) tile_end(t);
     }
+    // Tiles after this wave's last: keep joining the barriers and moving tiles.
+    for (int t = max(tlast + 1, 0); t < ntiles - 1; ++t) tile_end(t);
 
     const float sc = a.scale;
 #pragma unroll
@@ -929,14 +1039,14 @@ hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_
     const dim3 grid((unsigned)(nqblk * a.B * a.H)), block(256);
     if (causal) {
         if (dropout)
-            hipLaunchKernelGGL((bwd_dq_kernel<true, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dq_kernel<true, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, false>), grid, block, 0, st, a);
     } else {
         if (dropout)
-            hipLaunchKernelGGL((bwd_dq_kernel<false, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dq_kernel<false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, false>), grid, block, 0, st, a);
     }
     return hipGetLastError();
 }
