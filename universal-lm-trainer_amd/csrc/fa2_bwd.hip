@@ -178,6 +178,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     // multiple of the tile size, so only that tile can need a mask.
     const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32 * DQ_QB, S) - 1) / DQ_KT : ntiles - 1;
 
+    // Stage of tile t (t >= 0; unsigned, so a power-of-two count is a mask).
+    auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)QP_NST); };
     // Tile loader (direct global->LDS transfers): wave w moves transfers
     // j = 2w, 2w+1 of the K and the V tile; lane L of transfer j lands at
     // chunk position 64j + L = 8*row + (L & 7), row = 8j + (L >> 3), and
@@ -198,17 +200,26 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
             vo[i] = (uint32_t)(row * (int)a.vss + 8 * ch) * 2u;
         }
     };
-    auto issue = [&](int t) FA2_INLINE {
-        const int k0 = t * DQ_KT;
+    // Tiles are issued in order, once each: scalar running addresses (global
+    // tile bases, LDS stage) advance by a constant per tile.
+    uint64_t gk = (uint64_t)(uintptr_t)Kp, gv = (uint64_t)(uintptr_t)Vp;
+    const uint64_t k_step = (uint64_t)DQ_KT * a.kss * 2, v_step = (uint64_t)DQ_KT * a.vss * 2;
+    int kn = 0;          // first key of the next tile to issue
+    uint32_t stn = 0;    // its stage
+    const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 2048u * (uint32_t)wave;
+    auto issue = [&](int) FA2_INLINE {
         uint32_t ko[2], vo[2];
-        tile_offsets(k0, ko, vo);
-        const _Float16 *kb = Kp + (int64_t)k0 * a.kss;
-        const _Float16 *vb = Vp + (int64_t)k0 * a.vss;
+        tile_offsets(kn, ko, vo);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            lds_dma16(kb, ko[i], sKV[t % QP_NST][0] + 64 * (2 * wave + i));
-            lds_dma16(vb, vo[i], sKV[t % QP_NST][1] + 64 * (2 * wave + i));
+            const uint32_t d = lds_kv + stn * (uint32_t)sizeof(sKV[0]) + 1024u * (uint32_t)i;
+            lds_dma16_at(gk, ko[i], d);
+            lds_dma16_at(gv, vo[i], d + (uint32_t)sizeof(sKV[0][0]));
         }
+        gk += k_step;
+        gv += v_step;
+        kn += DQ_KT;
+        stn = (stn + 1 == QP_NST) ? 0 : stn + 1;
     };
 #pragma unroll
     for (int t = 0; t < QP_NST - 1; ++t)
@@ -347,7 +358,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         dsB[1] = zero_h8();
         int t = 0;
         for (; t < tlast; ++t) {
-            const int st = t % QP_NST, sp = (t + QP_NST - 1) % QP_NST, sn = (t + 1) % QP_NST;
+            const int st = stage_of(t), sp = stage_of(t + QP_NST - 1), sn = stage_of(t + 1);
             step(t, 0, 0, sA, dpA, dsA, t > 0 ? sp : st, 1, 1, dsB, st, 0, 1, sB, dpB);
             step(t, 0, 1, sB, dpB, dsB, st, 0, 0, dsA, st, 1, 0, sA, dpA);
             step(t, 1, 0, sA, dpA, dsA, st, 0, 1, dsB, st, 1, 1, sB, dpB);
@@ -355,7 +366,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
             step(t, 1, 1, sB, dpB, dsB, st, 1, 0, dsA, sn, 0, 0, sA, dpA);
         }
         // Tile tlast in serial order, masked where needed.
-        const int st = t % QP_NST, sp = (t + QP_NST - 1) % QP_NST;
+        const int st = stage_of(t), sp = stage_of(t + QP_NST - 1);
         const bool m = need_mask(t);
         if (m) {
             FA2_COLD_BRANCH();
@@ -770,17 +781,32 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         qo = (uint32_t)(row * (int)a.qss + 8 * tch) * 2u;     // strides < 2^24 (host check)
         doo = (uint32_t)(row * (int)a.doss + 8 * tch) * 2u;
     };
+    // Stage of tile t (t >= 0; unsigned, so a power-of-two count is a mask).
+    auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)KP_NST); };
     uint32_t qoff0, dooff0;
     tile_offsets(0, qoff0, dooff0);
     const uint32_t ldoff = ((lane < 32) ? (uint32_t)BH * (uint32_t)S * 4u : 0u) + 4u * (uint32_t)(lane & 31);
-    const float *ldbase = a.delta + (int64_t)bh * S;
-    auto issue = [&](int t) FA2_INLINE {
-        const int q0 = q_start + t * KP_QT;
+    // Tiles are issued in order, once each: scalar running addresses (global
+    // tile bases, LDS stage) advance by a constant per tile instead of being
+    // recomputed with 64-bit multiplies at every transfer.
+    uint64_t gq = (uint64_t)(uintptr_t)(Qp + (int64_t)q_start * a.qss);
+    uint64_t gdo = (uint64_t)(uintptr_t)(dOp + (int64_t)q_start * a.doss);
+    uint64_t gld = (uint64_t)(uintptr_t)(a.delta + (int64_t)bh * S + q_start);
+    const uint64_t dq_step = (uint64_t)KP_QT * a.qss * 2, ddo_step = (uint64_t)KP_QT * a.doss * 2;
+    int qn = q_start;          // first query of the next tile to issue
+    uint32_t stn = 0;          // its stage
+    const uint32_t lds_qd = lds_addr(&sQD[0][0][0]) + 1024u * (uint32_t)wave, lds_ld = lds_addr(&sLD[0][0]);
+    auto issue = [&](int) FA2_INLINE {
         uint32_t qo = qoff0, doo = dooff0;
-        if (q0 + KP_QT > S) tile_offsets(q0, qo, doo);
-        lds_dma16(Qp + (int64_t)q0 * a.qss, qo, sQD[t % KP_NST][0] + 64 * wave);
-        lds_dma16(dOp + (int64_t)q0 * a.doss, doo, sQD[t % KP_NST][1] + 64 * wave);
-        if (wave == 0) lds_dma4(ldbase + q0, ldoff, sLD[t % KP_NST]);
+        if (qn + KP_QT > S) tile_offsets(qn, qo, doo);
+        lds_dma16_at(gq, qo, lds_qd + stn * (uint32_t)sizeof(sQD[0]));
+        lds_dma16_at(gdo, doo, lds_qd + stn * (uint32_t)sizeof(sQD[0]) + (uint32_t)sizeof(sQD[0][0]));
+        if (wave == 0) lds_dma4_at(gld, ldoff, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
+        gq += dq_step;
+        gdo += ddo_step;
+        gld += KP_QT * sizeof(float);
+        qn += KP_QT;
+        stn = (stn + 1 == KP_NST) ? 0 : stn + 1;
     };
 #pragma unroll
     for (int t = 0; t < KP_NST - 1; ++t)
@@ -879,7 +905,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     auto pds_general = [&](int t, const f16x &s, const f16x &dp, h8(&pb)[2], h8(&dsb)[2]) FA2_INLINE {
         const int q0 = q_start + t * KP_QT;
         f4 l4[4], d4[4];
-        stats(t % KP_NST, l4, d4);
+        stats(stage_of(t), l4, d4);
         const int lo = key - q0 - 4 * g2;        // visible iff off >= lo (causal)
         const int hi = S - q0 - 4 * g2;          // and off < hi
 #pragma unroll
@@ -956,7 +982,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     };
     auto step = [&](int t, f16x &s_n, f16x &dp_n, const h8(&pb_p)[2], const h8(&ds_p)[2], const f16x &s_c,
                     const f16x &dp_c, h8(&pb_c)[2], h8(&ds_c)[2]) FA2_INLINE {
-        step_at(t, (t + KP_NST - 1) % KP_NST, t % KP_NST, (t + 1) % KP_NST, s_n, dp_n, pb_p, ds_p, s_c, dp_c,
+        step_at(t, stage_of(t + KP_NST - 1), stage_of(t), stage_of(t + 1), s_n, dp_n, pb_p, ds_p, s_c, dp_c,
                 pb_c, ds_c);
     };
 
@@ -971,10 +997,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     if (tfirst < ntiles) {
         // First tile: serial order, masked.
         const int t0 = tfirst;
-        sdp(t0 % KP_NST, sA, dpA);
+        sdp(stage_of(t0), sA, dpA);
         pds_general(t0, sA, dpA, pbA, dsA);
-        if (t0 + 1 < ntiles) sdp((t0 + 1) % KP_NST, sB, dpB);
-        if (t0 == tl) dkdv(t0 % KP_NST, pbA, dsA);
+        if (t0 + 1 < ntiles) sdp(stage_of(t0 + 1), sB, dpB);
+        if (t0 == tl) dkdv(stage_of(t0), pbA, dsA);
         tile_end(t0);
         int t = t0 + 1;
         for (; t + 1 < tl; t += 2) {   // roles B (t) and A (t + 1)
@@ -999,9 +1025,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                     pbA[hh] = pbB[hh]; dsA[hh] = dsB[hh]; pbB[hh] = tp; dsB[hh] = tq;
                 }
             }
-            dkdv((tl + KP_NST - 1) % KP_NST, pbB, dsB);   // tile tl - 1
+            dkdv(stage_of(tl + KP_NST - 1), pbB, dsB);   // tile tl - 1
             pds_general(tl, sA, dpA, pbA, dsA);
-            dkdv(tl % KP_NST, pbA, dsA);
+            dkdv(stage_of(tl), pbA, dsA);
             tile_end(tl);
         }
     }

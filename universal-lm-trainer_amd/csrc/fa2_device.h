@@ -187,6 +187,36 @@ __device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, void *
         : "v"(off), "s"(sb), "s"(lds));
 }
 
+// LDS byte address of a __shared__ object, for the forms below that take the
+// destination as an integer (converted once, outside the tile loop, instead
+// of a generic-to-LDS pointer conversion at every transfer).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const lds_void *)p;
+}
+
+// lds_dma16 / lds_dma4 with a wave-uniform 64-bit byte address and an LDS
+// byte address, both already scalar (no conversion or readfirstlane).
+__device__ __forceinline__ void lds_dma16_at(uint64_t base, uint32_t off, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds));
+}
+__device__ __forceinline__ void lds_dma4_at(uint64_t base, uint32_t off, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dword %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds));
+}
+
 // The 4-byte form (global_load_lds_dword): lane L writes 4 bytes to LDS
 // bytes [dst + 4*L, +4).
 __device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, void *dst) {

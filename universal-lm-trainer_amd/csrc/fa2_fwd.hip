@@ -123,20 +123,31 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
             vo[i] = (uint32_t)(row * (int)a.vss + 8 * vch) * 2u;
         }
     };
+    // Stage of tile t (t >= 0; unsigned, so a power-of-two count is a mask).
+    auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)NST); };
     uint32_t koffg[2], voffg[2];
     tile_offsets(0, koffg, voffg);
-    auto issue = [&](int t) FA2_INLINE {
-        const int k0 = t * KT;
+    // Tiles are issued in order, once each: scalar running addresses (global
+    // tile bases, LDS stage) advance by a constant per tile instead of being
+    // recomputed with 64-bit multiplies at every transfer.
+    uint64_t gk = (uint64_t)(uintptr_t)Kp, gv = (uint64_t)(uintptr_t)Vp;
+    const uint64_t k_step = (uint64_t)KT * a.kss * 2, v_step = (uint64_t)KT * a.vss * 2;
+    int kn = 0;          // first key of the next tile to issue
+    uint32_t stn = 0;    // its stage
+    const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 1024u * (uint32_t)(TPW * wave);
+    auto issue = [&](int) FA2_INLINE {
         uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
-        if (k0 + KT > S) tile_offsets(k0, ko, vo);
-        const _Float16 *kb = Kp + (int64_t)k0 * a.kss;
-        const _Float16 *vb = Vp + (int64_t)k0 * a.vss;
+        if (kn + KT > S) tile_offsets(kn, ko, vo);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
-            const int j = TPW * wave + i;
-            lds_dma16(kb, ko[i], sKV[t % NST][0] + 64 * j);
-            lds_dma16(vb, vo[i], sKV[t % NST][1] + 64 * j);
+            const uint32_t d = lds_kv + stn * (uint32_t)sizeof(sKV[0]) + 1024u * (uint32_t)i;
+            lds_dma16_at(gk, ko[i], d);
+            lds_dma16_at(gv, vo[i], d + (uint32_t)sizeof(sKV[0][0]));
         }
+        gk += k_step;
+        gv += v_step;
+        kn += KT;
+        stn = (stn + 1 == NST) ? 0 : stn + 1;
     };
 #pragma unroll
     for (int t = 0; t < NST - 1; ++t)
@@ -372,9 +383,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     auto steady = [&](int t, f16x(&s_cur)[QB][2], h8(&p_cur)[QB][2][2], f16x(&s_nxt)[QB][2],
                       h8(&p_prv)[QB][2][2]) FA2_INLINE {
         float rs[QB];
-        step((t + 1) % NST, (t + NST - 1) % NST, s_nxt, p_prv, s_cur, p_cur, rs);
+        step(stage_of(t + 1), stage_of(t + NST - 1), s_nxt, p_prv, s_cur, p_cur, rs);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) softmax_tail(qb, t * KT, t % NST, p_cur[qb], rs[qb]);
+        for (int qb = 0; qb < QB; ++qb) softmax_tail(qb, t * KT, stage_of(t), p_cur[qb], rs[qb]);
         tile_end(t);
     };
     // First tile, this wave's last (diagonal / tail) tile, and the tiles after
@@ -382,7 +393,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     auto general = [&](int t, f16x(&s_cur)[QB][2], h8(&p_cur)[QB][2][2], f16x(&s_nxt)[QB][2],
                        h8(&p_prv)[QB][2][2]) FA2_INLINE {
         const int k0 = t * KT;
-        if (t >= 1 && t - 1 <= tlast) pv((t + NST - 1) % NST, p_prv);
+        if (t >= 1 && t - 1 <= tlast) pv(stage_of(t + NST - 1), p_prv);
         if (t <= tlast) {
             // Serial order (rare path): each operand dies before the next
             // group's results are born, which keeps the register peak low.
@@ -392,10 +403,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
                     FA2_COLD_BRANCH();
                     mask(qb, k0, s_cur[qb]);
                 }
-                softmax_tail(qb, k0, t % NST, p_cur[qb], p_form(s_cur[qb], msc[qb], p_cur[qb]));
+                softmax_tail(qb, k0, stage_of(t), p_cur[qb], p_form(s_cur[qb], msc[qb], p_cur[qb]));
             }
-            if (t + 1 <= tlast) s_mm((t + 1) % NST, s_nxt);
-            if (t == ntiles - 1) pv(t % NST, p_cur);   // nothing after it drains P(t)
+            if (t + 1 <= tlast) s_mm(stage_of(t + 1), s_nxt);
+            if (t == ntiles - 1) pv(stage_of(t), p_cur);   // nothing after it drains P(t)
         }
         tile_end(t);
     };
