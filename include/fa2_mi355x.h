@@ -76,8 +76,9 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
  *     the accumulator with fp32 atomics, then dQ = scale * accumulator.
  *     Slower on MI355X (the atomics are L2-throughput bound); kept selectable.
  * The workspace (fa2_bwd_workspace_bytes) holds delta[b,h,i] = sum_d O*dO and
- * LSE[b,h,i] * log2(e) in fp32 (written by the dQ or delta step, read by the
- * dK/dV step) and the fp32 dQ accumulator.  B*H*S must be below 2^30. */
+ * LSE[b,h,i] * log2(e) in fp32, the same per-row terms as bf16 parts for the
+ * dK/dV step's MFMAs (all written by the dQ or delta step, read by the dK/dV
+ * step) and the fp32 dQ accumulator.  B*H*S must be below 2^30. */
 typedef struct fa2_bwd_params {
     const void *q, *k, *v, *o, *dout;   /* fp16 [B,H,S,64]                     */
     const float *lse;                   /* fp32 [B,H,S] from the forward       */
@@ -93,8 +94,9 @@ typedef struct fa2_bwd_params {
 } fa2_bwd_params;
 
 /* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta and scaled LSE
- * (8*B*H*S bytes, rounded up to 256) followed by the fp32 dQ accumulator
- * (256*B*H*S bytes). */
+ * (8*B*H*S bytes, rounded up to 256), the row terms -LSE*log2(e)/scale2 and
+ * -delta as three bf16 parts each (16*B*H*ceil32(S) bytes, rounded up to 256),
+ * then the fp32 dQ accumulator (256*B*H*S bytes). */
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S);
 
 int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,

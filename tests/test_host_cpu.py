@@ -83,7 +83,10 @@ def test_empty_problem_is_a_noop():
         p = _dummy_fwd(**{dim: 0})
         assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 0
     # fp32 delta rounded up to 256 bytes, then the fp32 dQ accumulator
-    assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 256 + 2 * 3 * 5 * 64 * 4
+    # fp32 delta and LSE (rounded to 256 B), bf16 row terms (16 B per query, S rounded to 32,
+    # rounded to 256 B), fp32 dQ accumulator
+    assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 256 + 2 * 3 * 32 * 16 + 2 * 3 * 5 * 64 * 4
+    assert lib.fa2_bwd_workspace_bytes(1, 1, 33) == 512 + 1024 + 33 * 64 * 4
     assert lib.fa2_bwd_workspace_bytes(0, 3, 5) == 0
 
 

@@ -29,6 +29,23 @@
 namespace fa2 {
 namespace {
 
+// Word index of query q's 8-byte slot for term `which` (0: -LSE*log2(e)/scale2,
+// 1: -delta) in the workspace's per-row bf16 parts: blocks of 512 bytes per
+// 32 queries of a (b,h), the 32 first terms then the 32 second terms.
+__device__ __forceinline__ int64_t trip_word(int S, int bh, int q, int which) {
+    const int nb = (S + 31) >> 5;
+    return ((int64_t)bh * nb + (q >> 5)) * 128 + which * 64 + 2 * (q & 31);
+}
+// Writes both terms of query q (lse2 = LSE * log2(e)).
+__device__ __forceinline__ void store_row_terms(const BwdArgs &a, int bh, int q, float lse2, float delta) {
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    uint32_t w0, w1;
+    split3_words(-lse2 / a.scale2, w0, w1);
+    *reinterpret_cast<u2v *>(a.trip + trip_word(a.S, bh, q, 0)) = u2v{w0, w1};
+    split3_words(-delta, w0, w1);
+    *reinterpret_cast<u2v *>(a.trip + trip_word(a.S, bh, q, 1)) = u2v{w0, w1};
+}
+
 // ---------------------------------------------------------------------------
 // delta only (used when the caller asks for delta without dQ): 8 lanes/row.
 // ---------------------------------------------------------------------------
@@ -51,7 +68,11 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const BwdArgs a) {
     sum += __shfl_xor(sum, 4);
     if (row < S && part == 0) {
         a.delta[(int64_t)bh * S + row] = sum;
-        if (a.lse) a.lse2[(int64_t)bh * S + row] = a.lse[b * a.lsb + h * a.lsh + row] * LOG2E;
+        if (a.lse) {
+            const float l2 = a.lse[b * a.lsb + h * a.lsh + row] * LOG2E;
+            a.lse2[(int64_t)bh * S + row] = l2;
+            store_row_terms(a, bh, row, l2, sum);
+        }
     }
     if (a.dqacc && row < S) {  // fused backward: clear this row of the fp32 dQ accumulator
         f4 *z = reinterpret_cast<f4 *>(a.dqacc + ((int64_t)bh * S + row) * HD + 8 * part);
@@ -149,9 +170,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         }
         dl[qb] = part + xor32(part);
         lse2[qb] = valid ? Lp[qr] * LOG2E : INFINITY;
-        if (valid && g2 == 0) {
+        if (valid && g2 == 0) {   // for the dK/dV pass
             Dp[q] = dl[qb];
-            a.lse2[(int64_t)bh * S + q] = lse2[qb];   // for the dK/dV pass
+            a.lse2[(int64_t)bh * S + q] = lse2[qb];
+            store_row_terms(a, bh, q, lse2[qb], dl[qb]);
         }
     }
 
@@ -720,10 +742,21 @@ static_assert(KP_NST >= 4 && KP_NST <= 6, "dK/dV stages");
 // while the VALU forms P and dS of tile t (reference @ None:
 // csrc/flash_attn_v100/flash_attn_v100_bwd.cu:300-470 computes the same
 // quantities per key tile).
-template <bool CAUSAL, bool DROPOUT>
+//
+// FOLD (no dropout; the host also requires scale2 >= 1e-20): the row terms
+// -lse2/scale2 and -delta enter the S and dP accumulators through one bf16
+// MFMA step each (their three bf16 parts, written by the dQ or delta pass,
+// against ones), so P = exp2(S*scale2) and dS = P * dP take no per-element
+// row statistics from LDS and no subtraction.  Otherwise the tile's lse2 and
+// delta are read from LDS per element.
+template <bool CAUSAL, bool DROPOUT, bool FOLD>
 __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
+    static_assert(!(FOLD && DROPOUT), "the folded row terms assume no dropout");
     __shared__ __attribute__((aligned(16))) h8 sQD[KP_NST][2][KP_QT * 8];   // Q, dO tiles (4 KB each)
-    __shared__ __attribute__((aligned(16))) float sLD[KP_NST][2 * KP_QT];   // lse2[32], delta[32]
+    // Per stage: lse2[32], delta[32] (fp32); FOLD: the 512-byte block of bf16
+    // row terms (and a duplicate from the transfer's upper 32 lanes).
+    __shared__ __attribute__((aligned(16))) float sLD[KP_NST][FOLD ? 256 : 2 * KP_QT];
+    __shared__ __attribute__((aligned(16))) uint32_t sZero[2];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -774,6 +807,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     // (L & 7) ^ swz_both(row) of query row q0 + row (rows past S: row S - 1,
     // masked on use).  Wave 0 also moves the tile's lse2 (lanes 0..31) and
     // delta (lanes 32..63) from the workspace, where lse2 = delta + B*H*S.
+    // FOLD: wave 0's lanes 0..31 move the tile's 512-byte block of row terms
+    // instead (lanes 32..63 repeat it into the stage's upper half).
     const int trow = 8 * wave + (lane >> 3);
     const int tch = (lane & 7) ^ swz_both(trow);
     auto tile_offsets = [&](int q0, uint32_t &qo, uint32_t &doo) FA2_INLINE {
@@ -791,7 +826,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     // recomputed with 64-bit multiplies at every transfer.
     uint64_t gq = (uint64_t)(uintptr_t)(Qp + (int64_t)q_start * a.qss);
     uint64_t gdo = (uint64_t)(uintptr_t)(dOp + (int64_t)q_start * a.doss);
-    uint64_t gld = (uint64_t)(uintptr_t)(a.delta + (int64_t)bh * S + q_start);
+    uint64_t gld = FOLD ? (uint64_t)(uintptr_t)(a.trip + trip_word(S, bh, q_start, 0))
+                        : (uint64_t)(uintptr_t)(a.delta + (int64_t)bh * S + q_start);
+    const uint32_t ldoff_t = FOLD ? 16u * (uint32_t)(lane & 31) : ldoff;
     const uint64_t dq_step = (uint64_t)KP_QT * a.qss * 2, ddo_step = (uint64_t)KP_QT * a.doss * 2;
     int qn = q_start;          // first query of the next tile to issue
     uint32_t stn = 0;          // its stage
@@ -801,10 +838,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         if (qn + KP_QT > S) tile_offsets(qn, qo, doo);
         lds_dma16_at(gq, qo, lds_qd + stn * (uint32_t)sizeof(sQD[0]));
         lds_dma16_at(gdo, doo, lds_qd + stn * (uint32_t)sizeof(sQD[0]) + (uint32_t)sizeof(sQD[0][0]));
-        if (wave == 0) lds_dma4_at(gld, ldoff, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
+        if (wave == 0) {
+            if (FOLD)
+                lds_dma16_at(gld, ldoff_t, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
+            else
+                lds_dma4_at(gld, ldoff_t, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
+        }
         gq += dq_step;
         gdo += ddo_step;
-        gld += KP_QT * sizeof(float);
+        gld += FOLD ? 512 : KP_QT * sizeof(float);
         qn += KP_QT;
         stn = (stn + 1 == KP_NST) ? 0 : stn + 1;
     };
@@ -845,6 +887,19 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         return tr_read8_both(reinterpret_cast<const _Float16 *>(sQD[stage][which]), toff[db][0], toff[db][1],
                              16 * hh);
     };
+    // FOLD: A operand of the bf16 step adding row term `which` of the tile in
+    // `stage` (lane (c, g2 = 0): the three parts of query row c in k = 0..2;
+    // lanes g2 = 1: zeros), and its B operand, ones in k = 0..2.
+    const b8 ones3 = g2 == 0 ? ones3_b8() : zero_b8();
+    auto aread = [&](int stage, int which) FA2_INLINE {
+        typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        const char *src = g2 == 0 ? reinterpret_cast<const char *>(sLD[stage]) + 256 * which + 8 * c
+                                  : reinterpret_cast<const char *>(sZero);
+        const u2v w = *reinterpret_cast<const u2v *>(src);
+        const u4v v = {w[0], w[1], 0u, 0u};
+        return __builtin_bit_cast(b8, v);
+    };
 
     // S = Q K^T and dP = dO V^T of the tile in `stage`: rows = the tile's
     // queries 8i + 4*g2 + j, column = this lane's key.
@@ -857,7 +912,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                 nq = rread(stage, 0, st + 1);
                 nd = rread(stage, 1, st + 1);
             }
-            if (st == 0) {
+            if (st == 0 && FOLD) {
+                s = mfma32(fq, kf[0], mfma32_bf16_first(aread(stage, 0), ones3));
+                dp = mfma32(fd, vf[0], mfma32_bf16_first(aread(stage, 1), ones3));
+            } else if (st == 0) {
                 s = mfma32_first(fq, kf[0]);
                 dp = mfma32_first(fd, vf[0]);
             } else {
@@ -880,7 +938,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     // P and dS of element r (query row q) of a tile, from its score s, dP
     // value g, lse2 l and delta dl.  Dropout: dV takes the kept, rescaled P;
     // dS = P * (dP * keep / (1-p) - delta).
+    // FOLD: s and g already hold S - lse2/scale2 and dP - delta.
     auto pds = [&](float sv, float g, float l, float dl, int q, float &pd, float &ds) FA2_INLINE {
+        if (FOLD) {
+            pd = __builtin_amdgcn_exp2f(sv * scale2);
+            ds = pd * g;
+            return;
+        }
         const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -l));
         if (DROPOUT) {
             const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
@@ -895,6 +959,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     auto stats = [&](int stage, f4(&l4)[4], f4(&d4)[4]) FA2_INLINE {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            if (FOLD) {   // unused
+                l4[i] = f4{0.f, 0.f, 0.f, 0.f};
+                d4[i] = l4[i];
+                continue;
+            }
             l4[i] = *reinterpret_cast<const f4 *>(&sLD[stage][8 * i + 4 * g2]);
             d4[i] = *reinterpret_cast<const f4 *>(&sLD[stage][KP_QT + 8 * i + 4 * g2]);
         }
@@ -935,6 +1004,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         const int q0 = q_start + t * KP_QT;
         f4 l4[4], d4[4];
         stats(sc_, l4, d4);
+        b8 al, ad;
+        if (FOLD) {
+            al = aread(sn, 0);
+            ad = aread(sn, 1);
+        }
         // chunk i < 4: dK/dV for (db, hh) = (i >> 1, i & 1); i >= 4: S/dP for d-step i - 4
         h8 n0 = tread(sp, 1, 0, 0), n1 = tread(sp, 0, 0, 0);
 #pragma unroll
@@ -951,6 +1025,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                 const int db = i >> 1, hh = i & 1;
                 dv[db] = mfma32(f0, pb_p[hh], dv[db]);
                 dk[db] = mfma32(f1, ds_p[hh], dk[db]);
+                if (FOLD && i == 3) {
+                    s_n = mfma32_bf16_first(al, ones3);
+                    dp_n = mfma32_bf16_first(ad, ones3);
+                }
+            } else if (i == 4 && FOLD) {
+                s_n = mfma32(f0, kf[0], s_n);
+                dp_n = mfma32(f1, vf[0], dp_n);
             } else if (i == 4) {
                 s_n = mfma32_first(f0, kf[0]);
                 dp_n = mfma32_first(f1, vf[0]);
@@ -990,6 +1071,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     f16x sA, dpA, sB, dpB;
     h8 pbA[2], dsA[2], pbB[2], dsB[2];
     const int tl = ntiles - 1;
+    if (FOLD && tid == 0) {   // the zero A-operand half of aread (published by the barrier below)
+        sZero[0] = 0u;
+        sZero[1] = 0u;
+    }
     // Initial wait: tiles 0 and 1 landed, tiles 2 .. NST-2 may be in flight.
     wait_tiles(min(KP_NST - 3, ntiles - 2));
     lds_barrier();
@@ -1097,16 +1182,22 @@ static void launch_dkv_t(const BwdArgs &a, bool causal, bool dropout, hipStream_
 hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const int nkblk = (a.S + KP_KWG - 1) / KP_KWG;
     const dim3 grid((unsigned)(nkblk * a.B * a.H)), block(256);
+    // The folded row terms need -lse2/scale2 finite (|lse2| < 3e18 at this bound).
+    const bool fold = !dropout && a.scale2 >= 1e-20f;
     if (causal) {
         if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, true, false>), grid, block, 0, st, a);
+        else if (fold)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false, true>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false, false>), grid, block, 0, st, a);
     } else {
         if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, true, false>), grid, block, 0, st, a);
+        else if (fold)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false, true>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false, false>), grid, block, 0, st, a);
     }
     return hipGetLastError();
 }

@@ -131,16 +131,20 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
     return FA2_OK;
 }
 
-// Workspace: fp32 delta [B*H*S] (rounded up to 256 bytes), then the fp32 dQ
-// accumulator [B*H*S*64] of the fused backward.
-// fp32 delta and log2-scaled LSE, [B*H*S] each, rounded up to 256 bytes.
+// Workspace: fp32 delta and log2-scaled LSE, [B*H*S] each (rounded up to 256
+// bytes); the per-row bf16 parts of -LSE*log2(e)/scale2 and -delta, 16 bytes
+// per query with S rounded up to 32 (rounded up to 256 bytes); then the fp32
+// dQ accumulator [B*H*S*64] of the fused backward.
 static size_t delta_bytes(int32_t B, int32_t H, int32_t S) {
     return ((size_t)B * H * S * 2 * sizeof(float) + 255) & ~(size_t)255;
+}
+static size_t terms_bytes(int32_t B, int32_t H, int32_t S) {
+    return ((size_t)B * H * (((size_t)S + 31) & ~(size_t)31) * 16 + 255) & ~(size_t)255;
 }
 
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S) {
     if (B <= 0 || H <= 0 || S <= 0) return 0;
-    return delta_bytes(B, H, S) + (size_t)B * H * S * FA2_HEAD_DIM * sizeof(float);
+    return delta_bytes(B, H, S) + terms_bytes(B, H, S) + (size_t)B * H * S * FA2_HEAD_DIM * sizeof(float);
 }
 
 int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t workspace_bytes, void *stream) {
@@ -194,7 +198,9 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     a.dv = static_cast<_Float16 *>(p->dv);
     a.delta = static_cast<float *>(workspace);
     a.lse2 = a.delta + (int64_t)p->B * p->H * p->S;
-    a.dqacc = fused ? reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S))
+    a.trip = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S));
+    a.dqacc = fused ? reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S) +
+                                                terms_bytes(p->B, p->H, p->S))
                     : nullptr;
     a.qsb = p->q_stride[0]; a.qsh = p->q_stride[1]; a.qss = p->q_stride[2];
     a.ksb = p->k_stride[0]; a.ksh = p->k_stride[1]; a.kss = p->k_stride[2];

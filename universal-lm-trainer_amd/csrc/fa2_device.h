@@ -108,6 +108,19 @@ __device__ __forceinline__ b8 split3_bf16(float x) {
     return z;
 }
 
+// The same three parts packed into 8 bytes (hi | mid << 16, lo), the form the
+// backward's workspace keeps them in.  A non-finite x keeps hi = x and zero
+// residuals (no inf - inf).
+__device__ __forceinline__ void split3_words(float x, uint32_t &w0, uint32_t &w1) {
+    const bool fin = __builtin_isfinite(x);
+    b8 z = split3_bf16(fin ? x : 0.f);
+    if (!fin) z[0] = (__bf16)x;
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const u4v w = __builtin_bit_cast(u4v, z);
+    w0 = w[0];
+    w1 = w[1];
+}
+
 // Transposing operand read (ds_read_b64_tr_b16).  From a row-major LDS tile
 // M[k][n] (row stride LD halves), lane 32*g2 + c receives
 //     M[k0 + 8*a + 4*g2 + j][n0 + c]   in slot e = 4*a + j  (a = 0..1, j = 0..3),
