@@ -114,6 +114,27 @@ def test_softmax_scales(fa, scale):
     check_against(f"scale={scale}", got, oracle_ref(q, k, v, do, True, scale))
 
 
+@pytest.mark.parametrize("scale,amp,S", [(1.0, 4.0, 97), (0.125, 4.0, 250), (1e-3, 1.0, 130), (1e-25, 1.0, 70)])
+def test_row_term_extremes(fa, scale, amp, S):
+    """Large logits (LSE up to ~10^2 in log2 units, so -LSE*log2e/scale2 is large) and tiny scales: the
+    dK/dV pass adds the row terms through bf16 MFMA steps for scale2 >= 1e-20 and subtracts them
+    per element below that (the 1e-25 case); S not a multiple of 32 exercises the last term block."""
+    say(f"case row terms scale={scale} amp={amp} S={S}")
+    q, k, v, do = rand_inputs(1, 2, S, seed=31)
+    q, k = (q.float() * amp).half(), (k.float() * amp).half()
+    got = run_kernel(fa, q, k, v, do, scale=scale)
+    ref = oracle_ref(q, k, v, do, True, scale)
+    if scale >= 1e-6:
+        check_against(f"row terms scale={scale} amp={amp}", got, ref)
+        return
+    # dQ and dK carry the factor scale (~1e-25): below fp16's range, they are zero in fp16 output
+    # like any fp16 kernel's; O, LSE and dV do not depend on it.
+    o, lse, dv = (got[i].float().cpu().numpy() for i in (0, 1, 4))
+    assert orc.max_abs(o, np.asarray(ref[0])) <= O_TOL
+    assert orc.max_abs(lse, np.asarray(ref[1])) <= LSE_TOL
+    assert orc.rel_l2(dv, np.asarray(ref[4], np.float64)) <= G_TOL
+
+
 @pytest.mark.parametrize("p,seed", [(0.1, 1), (0.5, 0xC0FFEE), (0.9, 42)])
 @pytest.mark.parametrize("mode", [7, 15])
 def test_dropout_vs_oracle(fa, p, seed, mode):
@@ -191,6 +212,38 @@ def test_capi_direct_matches_binding(fa):
     # delta left in the workspace equals rowsum(O * dO)
     delta = (o.float() * do.float()).sum(-1).reshape(-1)
     assert torch.allclose(ws[: B * H * S], delta, atol=1e-3, rtol=1e-3)
+
+
+def test_capi_split_modes(fa):
+    """dQ (mode 2) then dK/dV (mode 4) as two calls sharing one workspace give the bits of mode 7;
+    delta-only (mode 1) then mode 4 matches the oracle (its delta sums in another order)."""
+    say("case C ABI split modes")
+    lib = capi.load()
+    q, k, v, do = rand_inputs(1, 2, 231, seed=23)
+    B, H, S, _ = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    pf = capi.fwd_params(q, k, v, o, lse, 0.125)
+    assert lib.fa2_fwd_f16(ctypes.byref(pf), stream) == 0, lib.fa2_last_error()
+    nbytes = lib.fa2_bwd_workspace_bytes(B, H, S)
+    outs = {}
+    for name, modes in (("7", (7,)), ("2+4", (2, 4)), ("1+4", (1, 4))):
+        ws = torch.full((nbytes // 4,), float("nan"), device=DEV)   # nothing may be read unwritten
+        dq, dk, dv = (torch.zeros_like(q) for _ in range(3))
+        pb = capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, 0.125)
+        for m in modes:
+            assert lib.fa2_bwd_f16(ctypes.byref(pb), m, ws.data_ptr(), ws.numel() * 4, stream) == 0, \
+                lib.fa2_last_error()
+        torch.cuda.synchronize()
+        outs[name] = (dq, dk, dv)
+    for a, b in zip(outs["7"][1:], outs["2+4"][1:]):
+        assert torch.equal(a, b)
+    assert torch.equal(outs["7"][0], outs["2+4"][0])
+    ref = oracle_ref(q, k, v, do, True, 0.125)
+    for got, want, n in zip(outs["1+4"][1:], ref[3:], ("dK", "dV")):
+        e = orc.rel_l2(got.float().cpu().numpy(), np.asarray(want, np.float64))
+        assert e <= G_TOL, f"mode 1+4 {n} rel err {e}"
 
 
 def test_deterministic(fa):
