@@ -61,6 +61,19 @@ typedef struct fa2_fwd_params {
 
 int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
 
+/* Forward over a key/value sequence of its own length, for inference callers:
+ * a prefill chunk of S new queries against a KV cache of s_k rows, or decode
+ * (S = 1).  Same as fa2_fwd_f16 except that k and v are [B,H,s_k,64] (q, o
+ * and lse keep S rows) and, with causal set, key j is visible to query i iff
+ * j <= i + causal_offset: 0 is torch SDPA's is_causal alignment (top-left),
+ * s_k - S the KV-cache one (bottom-right: the chunk is the last S positions).
+ * A query that sees no key gets O = 0 and LSE = -inf.  s_k = S with
+ * causal_offset = 0 is fa2_fwd_f16, bit for bit.
+ * No counterpart in the reference, whose kernel is square-only: its inference
+ * paths call torch SDPA on exactly these shapes (reference @ None: inf.py:128-133,
+ * hf_template/modeling_universal_lm.py:149-153 with the masks of :228-251). */
+int fa2_fwd_kv_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, void *stream);
+
 /* Backward: dQ, dK, dV from Q, K, V, O, LSE and dO, recomputing P from LSE.
  * Replaces fav100::fa_bwd and its three kernels (delta, dQ, dK/dV)
  *   (reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:42-506).

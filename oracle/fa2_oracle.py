@@ -16,6 +16,11 @@ How each function is pinned (tests/test_oracle.py):
   attention_dense_fwd  torch SDPA MATH backend (fp64, a library routine) on the same
                        inputs; closed forms (row 0 = V0; Q = 0 gives the cumulative
                        mean and LSE_i = ln(i+1)); brute force on tiny shapes.
+                       Non-square (causal_offset): SDPA MATH with the explicit
+                       boolean mask and with is_causal (top-left, offset 0); a
+                       bottom-right chunk equals the last rows of the square
+                       causal result; decode (one query, all keys visible) equals
+                       softmax(q K^T) V from scipy.
   attention_tiled_fwd  the dense oracle (fp64, ~1e-12) including tails (S % 64 != 0)
                        and the -inf / l = 0 guards.
   attention_bwd        torch autograd of SDPA MATH (fp64); invariants (rows of dS sum
@@ -87,25 +92,30 @@ def next_seed(initial_seed, counter):
 # ---------------------------------------------------------------------------
 # forward
 # ---------------------------------------------------------------------------
-def _visible(S, causal):
+def _visible(S, causal, Sk=None, causal_offset=0):
+    """[S, Sk] visibility: key j visible to query i iff j <= i + causal_offset (causal)."""
+    Sk = S if Sk is None else Sk
     if not causal:
-        return np.ones((S, S), dtype=bool)
-    return np.tril(np.ones((S, S), dtype=bool))
+        return np.ones((S, Sk), dtype=bool)
+    return np.arange(Sk)[None, :] <= np.arange(S)[:, None] + causal_offset
 
 
-def attention_dense_fwd(q, k, v, causal=True, scale=None, keep=None, p=0.0):
-    """Dense fp64 attention.  q,k,v: [B,H,S,D].  Returns (O, LSE).
+def attention_dense_fwd(q, k, v, causal=True, scale=None, keep=None, p=0.0, causal_offset=0):
+    """Dense fp64 attention.  q: [B,H,S,D], k, v: [B,H,Sk,D] (Sk = S in the
+    reference's square case).  Returns (O, LSE).
 
     LSE is the natural-log logsumexp of the scaled visible scores (-inf if a
     row sees nothing, flash_attn_v100.cu:283-287); P uses the un-dropped
     softmax and dropout multiplies it by keep/(1-p) (flash_attn_v100.cu:208-231);
-    a row with l = 0 gives O = 0 (:280)."""
+    a row with l = 0 gives O = 0 (:280).  causal_offset generalises the mask to
+    non-square inputs (key j visible to query i iff j <= i + causal_offset),
+    the fa2_fwd_kv_f16 contract; the reference itself is square-only."""
     q, k, v = (np.asarray(t, np.float64) for t in (q, k, v))
     S, D = q.shape[-2], q.shape[-1]
     if scale is None:
         scale = D ** -0.5
     s = np.einsum("bhid,bhjd->bhij", q, k) * scale
-    vis = _visible(S, causal)
+    vis = _visible(S, causal, k.shape[-2], causal_offset)
     s = np.where(vis, s, -np.inf)
     m = s.max(axis=-1, keepdims=True)
     m_safe = np.where(np.isfinite(m), m, 0.0)

@@ -77,12 +77,22 @@ def test_fwd_validation_rejects_before_launch(field, value, status):
     assert lib.fa2_status_string(rc) != b"unknown status"
 
 
+@pytest.mark.parametrize("s_k,coff,status", [(0, 0, 2), (-5, 0, 2), (16, (1 << 30) + 1, 4), (16, -(1 << 30) - 1, 4)])
+def test_fwd_kv_validation_rejects_before_launch(s_k, coff, status):
+    lib = capi.load()
+    p = _dummy_fwd()
+    rc = lib.fa2_fwd_kv_f16(ctypes.byref(p), s_k, coff, None)
+    assert rc == status, (rc, lib.fa2_last_error())
+    # B*H*s_k must fit the kernels' int32 row indices
+    p = _dummy_fwd()
+    assert lib.fa2_fwd_kv_f16(ctypes.byref(p), 1 << 28, 0, None) == 2
+
+
 def test_empty_problem_is_a_noop():
     lib = capi.load()
     for dim in ("B", "H", "S"):
         p = _dummy_fwd(**{dim: 0})
         assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 0
-    # fp32 delta rounded up to 256 bytes, then the fp32 dQ accumulator
     # fp32 delta and LSE (rounded to 256 B), bf16 row terms (16 B per query, S rounded to 32,
     # rounded to 256 B), fp32 dQ accumulator
     assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 256 + 2 * 3 * 32 * 16 + 2 * 3 * 5 * 64 * 4

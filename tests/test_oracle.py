@@ -263,3 +263,57 @@ def test_oracle_reproduces_golden_fixtures():
         _, seed, bh = key.split("/")
         rows, cols = np.arange(64).reshape(64, 1), np.arange(64).reshape(1, 64)
         assert np.array_equal(np.packbits(orc.dropout_keep(int(seed), rows, cols, int(bh), 0.1).reshape(-1)), z[key])
+
+
+# ---------------------------------------------------------------------------
+# Non-square forward (fa2_fwd_kv_f16's contract: key j visible to query i iff
+# j <= i + causal_offset)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("Sq,Sk,coff", [(1, 70, 69), (5, 70, 65), (37, 130, 93), (64, 64, 0),
+                                        (20, 150, 0), (90, 40, 0), (60, 25, -35), (33, 100, 10)])
+def test_kv_fwd_matches_sdpa_math_with_explicit_mask(Sq, Sk, coff):
+    q = _rand((1, 2, Sq, 64), 3 * Sq + Sk)
+    k, v = (_rand((1, 2, Sk, 64), 5 * Sk + i) for i in range(2))
+    o, lse = orc.attention_dense_fwd(q, k, v, causal=True, causal_offset=coff)
+    vis = torch.arange(Sk)[None, :] <= torch.arange(Sq)[:, None] + coff
+    tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
+    with sdpa_kernel(SDPBackend.MATH):
+        ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=vis).numpy()
+    s = torch.einsum("bhid,bhjd->bhij", tq, tk) * 0.125
+    ref_lse = torch.logsumexp(s.masked_fill(~vis, float("-inf")), dim=-1).numpy()
+    seen = vis.any(dim=1).numpy()          # rows that see no key: SDPA gives NaN, the contract 0 / -inf
+    assert orc.max_abs(o[..., seen, :], ref[..., seen, :]) < 1e-12
+    assert orc.max_abs(lse[..., seen], ref_lse[..., seen]) < 1e-12
+    assert np.all(o[..., ~seen, :] == 0.0) and np.all(lse[..., ~seen] == -np.inf)
+
+
+@pytest.mark.parametrize("Sq,Sk", [(20, 150), (90, 40), (1, 33)])
+def test_kv_fwd_offset_zero_is_sdpa_is_causal(Sq, Sk):
+    """torch SDPA's is_causal on non-square inputs aligns the mask top-left: offset 0."""
+    q = _rand((1, 1, Sq, 64), Sq)
+    k, v = (_rand((1, 1, Sk, 64), Sk + i) for i in range(2))
+    o, _ = orc.attention_dense_fwd(q, k, v, causal=True, causal_offset=0)
+    tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
+    assert orc.max_abs(o, _sdpa_math(tq, tk, tv, True).numpy()) < 1e-12
+
+
+@pytest.mark.parametrize("Sq,Sk", [(1, 70), (16, 200), (64, 64), (100, 129)])
+def test_kv_fwd_bottom_right_chunk_is_tail_of_square(Sq, Sk):
+    """A chunk of the last Sq queries against all Sk keys with offset Sk - Sq gives the last Sq rows
+    of the square causal attention (what a KV cache must reproduce)."""
+    qf, k, v = (_rand((1, 2, Sk, 64), 17 * Sk + i) for i in range(3))
+    of, lf = orc.attention_dense_fwd(qf, k, v, causal=True)
+    oc, lc = orc.attention_dense_fwd(qf[..., Sk - Sq:, :], k, v, causal=True, causal_offset=Sk - Sq)
+    assert orc.max_abs(oc, of[..., Sk - Sq:, :]) < 1e-12
+    assert orc.max_abs(lc, lf[..., Sk - Sq:]) < 1e-12
+
+
+def test_kv_fwd_decode_closed_form():
+    """One query against every key: softmax(q K^T * scale) V (scipy's softmax, a library routine)."""
+    from scipy.special import logsumexp, softmax
+    q = _rand((2, 3, 1, 64), 1)
+    k, v = (_rand((2, 3, 257, 64), 2 + i) for i in range(2))
+    o, lse = orc.attention_dense_fwd(q, k, v, causal=False, scale=0.2)
+    s = np.einsum("bhid,bhjd->bhij", q, k) * 0.2
+    assert orc.max_abs(o, np.einsum("bhij,bhjd->bhid", softmax(s, axis=-1), v)) < 1e-12
+    assert orc.max_abs(lse, logsumexp(s, axis=-1)) < 1e-12

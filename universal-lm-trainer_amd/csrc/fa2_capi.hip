@@ -92,16 +92,21 @@ const char *fa2_last_error(void) { return g_err; }
 
 const char *fa2_version(void) { return "fa2_mi355x 0.1 (gfx950, fp16 MFMA 32x32x16)"; }
 
-int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
-    g_err[0] = 0;
+// The forward over s_k key rows with key j visible to query i iff
+// j <= i + coff (causal); fa2_fwd_f16 is s_k = S, coff = 0.
+static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *stream) {
     if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
     int rc = check_shape(p->B, p->H, p->S, p->D, 256);
     if (rc) return rc;
     if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
     if ((int64_t)p->B * p->H * p->S == 0) return FA2_OK;
+    if (s_k < 1 || (double)p->B * p->H * s_k > 2147483647.0)
+        return fail(FA2_ERR_BAD_SHAPE, "key length %d outside 1 .. 2^31 / (B*H)", s_k);
+    if (coff < -(1 << 30) || coff > (1 << 30))
+        return fail(FA2_ERR_BAD_ARGUMENT, "causal offset %d outside +-2^30", coff);
     if ((rc = check_tensor("q", p->q, p->q_stride, p->B, p->H, p->S, true))) return rc;
-    if ((rc = check_tensor("k", p->k, p->k_stride, p->B, p->H, p->S, true))) return rc;
-    if ((rc = check_tensor("v", p->v, p->v_stride, p->B, p->H, p->S, true))) return rc;
+    if ((rc = check_tensor("k", p->k, p->k_stride, p->B, p->H, s_k, true))) return rc;
+    if ((rc = check_tensor("v", p->v, p->v_stride, p->B, p->H, s_k, true))) return rc;
     if ((rc = check_tensor("o", p->o, p->o_stride, p->B, p->H, p->S, false))) return rc;
     if (!aligned16(p->o) || (p->o_stride[0] | p->o_stride[1] | p->o_stride[2]) % 4)
         return fail(FA2_ERR_MISALIGNED, "o needs 16-byte base alignment and strides that are multiples of 4");
@@ -121,6 +126,8 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
     a.osb = p->o_stride[0]; a.osh = p->o_stride[1]; a.oss = p->o_stride[2];
     a.lsb = p->lse_stride[0]; a.lsh = p->lse_stride[1];
     a.B = p->B; a.H = p->H; a.S = p->S;
+    a.Sk = s_k;
+    a.coff = coff;
     a.scale2 = scale2_of(p->softmax_scale);
     a.negate = p->softmax_scale < 0.f;
     a.seed = p->seed;
@@ -129,6 +136,16 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
     const hipError_t e = fa2::launch_fwd(a, p->causal != 0, p->dropout_p > 0.f, (hipStream_t)stream);
     if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "forward launch: %s", hipGetErrorString(e));
     return FA2_OK;
+}
+
+int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
+    g_err[0] = 0;
+    return fwd_common(p, p ? p->S : 0, 0, stream);
+}
+
+int fa2_fwd_kv_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, void *stream) {
+    g_err[0] = 0;
+    return fwd_common(p, s_k, causal_offset, stream);
 }
 
 // Workspace: fp32 delta and log2-scaled LSE, [B*H*S] each (rounded up to 256

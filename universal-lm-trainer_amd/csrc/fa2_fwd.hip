@@ -65,7 +65,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
     const int lane = tid & 63, c = lane & 31, g2 = lane >> 5;
-    const int S = a.S;
+    const int S = a.S;       // query rows
+    const int Sk = a.Sk;     // key rows
+    const int coff = a.coff; // causal: key j visible to query i iff j <= i + coff
     const int BH = a.B * a.H;
     const int nqblk = (S + QWG - 1) / QWG;
     const int L = blockIdx.x;
@@ -83,11 +85,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     const int qw0 = q_wg0 + wave * 32 * QB;   // this wave's queries: qw0 .. qw0 + 32*QB - 1
     const float scale2 = a.scale2;
 
-    const int kend = CAUSAL ? min(S, q_wg0 + QWG) : S;
-    const int ntiles = (kend + KT - 1) / KT;
+    const int kend = CAUSAL ? min(Sk, q_wg0 + QWG + coff) : Sk;
+    const int ntiles = kend > 0 ? (kend + KT - 1) / KT : 0;
     // Last key tile this wave computes (-1: none).  Every wave still joins
     // every barrier and moves its share of every tile.
-    const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32 * QB, S) - 1) / KT : ntiles - 1;
+    const int kw_end = CAUSAL ? min(qw0 + 32 * QB + coff, Sk) : Sk;   // keys the wave's queries reach
+    const int tlast = (qw0 >= S || kw_end <= 0) ? -1 : (kw_end - 1) / KT;
+    // Tiles before tsteady are visible to every query of the wave (the
+    // steady, mask-free path); the rest run the general path.
+    const int tsteady = CAUSAL ? min(tlast, max(qw0 + coff + 1, 0) / KT) : tlast;
 
     // Q^T operand of d-step st: lane holds Q[q][16*st + 8*g2 + e].  Rows past
     // S load row S - 1 (unconditional loads stay in flight together); those
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // transfer j lands at chunk position 64j + L = 8*row + (L & 7) with
     // row = 8j + (L >> 3), so it fetches logical chunk (L & 7) ^ swz(row) of
     // key row k0 + row.  The lane's byte offsets within a tile are fixed; only
-    // the last tile, whose rows past S are redirected to row S - 1 (any
+    // the last tile, whose rows past Sk are redirected to row Sk - 1 (any
     // finite row: their scores are masked and their P is zero), needs them
     // recomputed.
     const int lrow = lane >> 3;
@@ -118,7 +124,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     auto tile_offsets = [&](int k0, uint32_t(&ko)[2], uint32_t(&vo)[2]) FA2_INLINE {
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
-            const int row = min(k0 + 8 * (TPW * wave + i) + lrow, S - 1) - k0;
+            const int row = min(k0 + 8 * (TPW * wave + i) + lrow, Sk - 1) - k0;
             ko[i] = (uint32_t)(row * (int)a.kss + 8 * kch[(TPW * wave + i) & 1]) * 2u;   // kss < 2^24 (host check)
             vo[i] = (uint32_t)(row * (int)a.vss + 8 * vch) * 2u;
         }
@@ -137,7 +143,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 1024u * (uint32_t)(TPW * wave);
     auto issue = [&](int) FA2_INLINE {
         uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
-        if (kn + KT > S) tile_offsets(kn, ko, vo);
+        if (kn + KT > Sk) tile_offsets(kn, ko, vo);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
             const uint32_t d = lds_kv + stn * (uint32_t)sizeof(sKV[0]) + 1024u * (uint32_t)i;
@@ -223,12 +229,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // Tail keys (>= S) and the causal triangle -> -inf.  key = k0 + 32*kb +
+    // Tail keys (>= Sk) and the causal triangle -> -inf.  key = k0 + 32*kb +
     // 4*g2 + (8*(r>>2) + (r&3)) is visible iff key <= lim; compared as a
     // constant against a per-lane bound, so no key index is materialised.
-    auto need_mask = [&](int k0) FA2_INLINE { return (k0 + KT > S) || (CAUSAL && k0 + KT - 1 > qw0); };
+    auto need_mask = [&](int k0) FA2_INLINE {
+        return (k0 + KT > Sk) || (CAUSAL && k0 + KT - 1 > qw0 + coff);
+    };
     auto mask = [&](int qb, int k0, f16x(&s)[2]) FA2_INLINE {
-        const int lim = CAUSAL ? min(qw0 + 32 * qb + c, S - 1) : S - 1;
+        const int lim = CAUSAL ? min(qw0 + 32 * qb + c + coff, Sk - 1) : Sk - 1;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             const int bound = lim - k0 - 32 * kb - 4 * g2;
@@ -378,7 +386,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         lds_barrier();
         if (t + NST - 1 < ntiles) issue(t + NST - 1);
     };
-    // Steady state (1 <= t < tlast): no masking -- the tile is below this
+    // Steady state (1 <= t < tsteady): no masking -- the tile is below this
     // wave's diagonal and not the last one -- and every group present.
     auto steady = [&](int t, f16x(&s_cur)[QB][2], h8(&p_cur)[QB][2][2], f16x(&s_nxt)[QB][2],
                       h8(&p_prv)[QB][2][2]) FA2_INLINE {
@@ -415,11 +423,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // would make the compiler select between whole register arrays.
     if (ntiles > 0) general(0, s0, p0, s1, p1);
     int t = 1;
-    for (; t + 1 < tlast; t += 2) {   // t odd, t + 1 even
+    for (; t + 1 < tsteady; t += 2) {   // t odd, t + 1 even
         steady(t, s1, p1, s0, p0);
         steady(t + 1, s0, p0, s1, p1);
     }
-    if (t < tlast) {                   // t odd
+    if (t < tsteady) {                   // t odd
         steady(t, s1, p1, s0, p0);
         ++t;
     }

@@ -15,7 +15,9 @@ struct FwdArgs {
     _Float16 *o;
     float *lse;
     int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss, osb, osh, oss, lsb, lsh;
-    int B, H, S;
+    int B, H, S;         // S: query rows (q, o, lse)
+    int Sk;              // key / value rows
+    int coff;            // causal: key j visible to query i iff j <= i + coff
     float scale2;        // |softmax_scale| * log2(e), at least FLT_MIN
     int negate;          // softmax_scale < 0: the Q operand is negated
     uint32_t seed;       // dropout hash seed

@@ -3,6 +3,10 @@
 // Exposes the reference's four extension ops with their signatures and
 // output conventions (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:386-397):
 //   fa_fwd(q, k, v, dropout_p, causal, softmax_scale, seed)            -> [o, lse]
+// plus, for inference callers (no reference counterpart; fa2_fwd_kv_f16):
+//   fa_fwd_kv(q, k, v, causal, softmax_scale, causal_offset)           -> [o, lse]
+// with k, v of their own sequence length and key j visible to query i iff
+// j <= i + causal_offset when causal.
 //   fa_bwd(q, k, v, o, lse, do, dropout_p, causal, softmax_scale, seed,
 //          mode=7)                                                      -> [dq, dk, dv]
 //   rope_fwd(q, k, cos, sin)                                            -> [qo, ko]
@@ -49,9 +53,10 @@ void check_qkv(const torch::Tensor &q, const torch::Tensor &k, const torch::Tens
     TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1, "last dim must be contiguous");
 }
 
-std::vector<torch::Tensor> fa_fwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, double dropout_p, bool causal,
-                                  double softmax_scale, int64_t seed) {
-    check_qkv(q, k, v);
+// The forward through fa2_fwd_kv_f16 (s_k = k's length); fa_fwd is the square case.
+std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor &k, const torch::Tensor &v,
+                                    double dropout_p, bool causal, double softmax_scale, int64_t seed,
+                                    int64_t causal_offset, const char *op) {
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     const int64_t B = q.size(0), H = q.size(1), S = q.size(2);
     // O follows q's memory order the way an eager elementwise output would:
@@ -85,8 +90,31 @@ std::vector<torch::Tensor> fa_fwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     p.dropout_p = (float)dropout_p;
     p.seed = (uint32_t)seed;
     p.causal = causal ? 1 : 0;
-    check_status(fa2_fwd_f16(&p, current_stream(q)), "fa_fwd");
+    TORCH_CHECK(k.size(2) <= INT32_MAX && causal_offset >= INT32_MIN && causal_offset <= INT32_MAX,
+                op, ": key length / causal offset out of range");
+    check_status(fa2_fwd_kv_f16(&p, (int32_t)k.size(2), (int32_t)causal_offset, current_stream(q)), op);
     return {o, lse};
+}
+
+std::vector<torch::Tensor> fa_fwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, double dropout_p, bool causal,
+                                  double softmax_scale, int64_t seed) {
+    check_qkv(q, k, v);
+    return fwd_impl(q, k, v, dropout_p, causal, softmax_scale, seed, 0, "fa_fwd");
+}
+
+std::vector<torch::Tensor> fa_fwd_kv(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal,
+                                     double softmax_scale, int64_t causal_offset) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "inputs must be on the GPU");
+    TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
+                "only fp16 supported");
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "q, k, v must be (B,H,S,D)");
+    TORCH_CHECK(q.size(3) == 64 && k.size(3) == 64 && v.size(3) == 64, "head_dim must be 64");
+    TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == q.size(0) && k.size(1) == q.size(1),
+                "k/v must be (B,H,S_k,64) with q's B and H");
+    TORCH_CHECK(k.size(2) >= 1, "empty key sequence");
+    TORCH_CHECK(k.device() == q.device() && v.device() == q.device(), "q/k/v device mismatch");
+    TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1, "last dim must be contiguous");
+    return fwd_impl(q, k, v, 0.0, causal, softmax_scale, 0, causal_offset, "fa_fwd_kv");
 }
 
 std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor o,
@@ -233,6 +261,9 @@ std::vector<torch::Tensor> rope_bwd(torch::Tensor dqo, torch::Tensor dko, torch:
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("fa_fwd", &fa_fwd, "FA2 forward (gfx950 MFMA)");
+    m.def("fa_fwd_kv", &fa_fwd_kv, "FA2 forward, k/v of their own length (inference)", pybind11::arg("q"),
+          pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("causal"), pybind11::arg("softmax_scale"),
+          pybind11::arg("causal_offset"));
     m.def("fa_bwd", &fa_bwd, "FA2 backward (gfx950 MFMA)", pybind11::arg("q"), pybind11::arg("k"),
           pybind11::arg("v"), pybind11::arg("o"), pybind11::arg("lse"), pybind11::arg("do"),
           pybind11::arg("dropout_p"), pybind11::arg("causal"), pybind11::arg("softmax_scale"),

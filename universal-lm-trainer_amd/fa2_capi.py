@@ -72,6 +72,8 @@ def load():
         lib = ctypes.CDLL(LIB)
         lib.fa2_fwd_f16.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_void_p]
         lib.fa2_fwd_f16.restype = ctypes.c_int
+        lib.fa2_fwd_kv_f16.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
+        lib.fa2_fwd_kv_f16.restype = ctypes.c_int
         lib.fa2_bwd_f16.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int32, ctypes.c_void_p,
                                     ctypes.c_size_t, ctypes.c_void_p]
         lib.fa2_bwd_f16.restype = ctypes.c_int

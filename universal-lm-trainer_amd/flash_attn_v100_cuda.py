@@ -23,10 +23,19 @@ Differences of mechanism, not of contract:
     stricter 32-byte predicate so the same tensors are routed the same way.
 
 Additions used by inference callers (``inf.py:128-133``,
-``hf_template/modeling_universal_lm.py:149-153``): ``sdpa(...)`` has the
-signature of ``torch.nn.functional.scaled_dot_product_attention`` and
-dispatches to the kernel only when ``attn_mask is None and is_causal`` and
-``can_use`` holds; otherwise it calls SDPA unchanged.
+``hf_template/modeling_universal_lm.py:149-153``):
+  * ``sdpa(...)`` has the signature of
+    ``torch.nn.functional.scaled_dot_product_attention``.  With no mask it
+    sends the causal, ``can_use`` case to ``flash_attn_v100`` (training,
+    differentiable) and, when no gradient is needed and there is no dropout,
+    any other fp16 head-64 shape -- non-causal, or ``S_q != S_k`` such as
+    decode against a KV cache -- to the forward kernel with SDPA's semantics
+    (``is_causal`` aligned top-left).  Everything else calls SDPA unchanged.
+  * ``flash_attn_kvcache(q, k, v, causal=True)``: forward-only attention of a
+    chunk of ``S_q`` new queries against ``S_k`` cached keys with the causal
+    mask aligned bottom-right (the chunk is the last ``S_q`` positions), the
+    mask the HF template builds by hand for KV-cache chunks
+    (``hf_template/modeling_universal_lm.py:228-246``).
 """
 
 import glob
@@ -195,14 +204,52 @@ def _disabled():
     return os.environ.get("FA_V100_DISABLE", "0") == "1"
 
 
+def _needs_grad(*ts):
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
+def _kv_ready(q, k, v):
+    """fp16 (B,H,S_q,64) queries against (B,H,S_k,64) keys/values, kernel-aligned."""
+    return (_fa_ready(q) and _fa_ready(k) and _fa_ready(v) and k.shape == v.shape
+            and k.shape[:2] == q.shape[:2] and k.size(2) >= 1)
+
+
+def _fwd_kv(q, k, v, causal, softmax_scale, causal_offset):
+    if not (q.is_cuda and q.dtype == torch.float16 and q.dim() == 4 and q.size(3) == 64):
+        raise ValueError("fp16 GPU tensors (B,H,S,64) only")
+    if _needs_grad(q, k, v):
+        raise RuntimeError("the key/value-length forward is inference-only (no backward)")
+    q, k, v = (t if _fa_ready(t) else t.contiguous() for t in (q, k, v))
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** -0.5
+    o, _ = extension().fa_fwd_kv(q, k, v, bool(causal), float(softmax_scale), int(causal_offset))
+    return o
+
+
+def flash_attn_kvcache(q, k, v, causal: bool = True, softmax_scale=None):
+    """Attention of q (B,H,S_q,64) against k, v (B,H,S_k,64), forward only, for
+    inference: a prefill chunk against a KV cache, or decode (S_q = 1).  With
+    causal, query i sees keys j <= i + S_k - S_q (the chunk is the last S_q
+    positions: the mask of hf_template/modeling_universal_lm.py:228-246); a
+    query that sees no key (S_q > S_k) gets zeros.  No reference counterpart:
+    the reference's kernel is square-only and these callers use SDPA."""
+    return _fwd_kv(q, k, v, causal, softmax_scale, k.size(2) - q.size(2))
+
+
 def sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None, **kwargs):
-    """Signature of ``F.scaled_dot_product_attention`` that routes the causal,
-    mask-free, kernel-eligible case to ``flash_attn_v100`` and everything else
-    to SDPA unchanged (the decision of train.py:1946-1961)."""
-    if (attn_mask is None and is_causal and not kwargs and not _disabled() and is_available()
-            and query.dim() == 4 and can_use(query, key, value)):
+    """Signature of ``F.scaled_dot_product_attention``.  Mask-free calls go to
+    the kernels: the causal ``can_use`` case through ``flash_attn_v100`` (the
+    decision of train.py:1946-1961), and, when no gradient is needed and
+    dropout is 0, other fp16 head-64 shapes (non-causal, S_q != S_k) through
+    the forward with SDPA's semantics.  Everything else calls SDPA unchanged."""
+    eligible = attn_mask is None and not kwargs and not _disabled() and is_available() and query.dim() == 4
+    if eligible and is_causal and can_use(query, key, value):
         return flash_attn_v100(query, key, value, dropout_p=dropout_p, causal=True,
                                softmax_scale=scale)
+    if (eligible and dropout_p == 0.0 and query.dtype == torch.float16 and query.size(3) == 64
+            and _kv_ready(query, key, value) and not _needs_grad(query, key, value)):
+        # SDPA semantics: is_causal on S_q != S_k aligns the mask top-left (offset 0).
+        return _fwd_kv(query, key, value, is_causal, scale, 0)
     return F.scaled_dot_product_attention(query, key, value, attn_mask=attn_mask,
                                           dropout_p=dropout_p, is_causal=is_causal,
                                           scale=scale, **kwargs)
