@@ -42,8 +42,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="2",
-                    help="2, 3-512, 3-1024, 3-2048, 3-4096, 4, or 5 (10-layer decoder training step "
-                         "with attention timed inside it)")
+                    help="2, 3-512, 3-1024, 3-2048, 3-4096, 4, 5 (10-layer decoder training step "
+                         "with attention timed inside it), kv-chunk (inference: 512 new queries "
+                         "against a 4096-key cache, bottom-right causal, forward only) or kv-decode "
+                         "(one query against a 4096-key cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
     ap.add_argument("--bwd-mode", type=int, default=7,
@@ -242,6 +244,60 @@ def decoder_step(args, torch, fa):
     }
 
 
+def kv_forward(args, torch, fa):
+    """Inference shapes of fa2_fwd_kv_f16 at B=8, H=12, D=64 against a 4096-key cache: a
+    512-query prefill chunk (bottom-right causal; MFMA-bound, TFLOP/s) or decode (one query;
+    HBM-bound, GB/s of K and V read).  Forward only; parity on two heads vs SDPA fp32."""
+    import torch.nn.functional as F
+    B, H, Sk = 8, 12, 4096
+    Sq = 512 if args.config == "kv-chunk" else 1
+    causal = Sq > 1
+    g = torch.Generator().manual_seed(0)
+    q = (torch.randn(B, H, Sq, 64, generator=g) * 0.5).half().cuda()
+    k, v = ((torch.randn(B, H, Sk, 64, generator=g) * 0.5).half().cuda() for _ in range(2))
+    ext = fa.extension()
+    coff = Sk - Sq
+    o, _ = ext.fa_fwd_kv(q, k, v, causal, 0.125, coff)
+    vis = torch.arange(Sk, device="cuda")[None, :] <= torch.arange(Sq, device="cuda")[:, None] + coff
+    worst = 0.0
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        ref = F.scaled_dot_product_attention(q[b:b + 1, h:h + 1].float(), k[b:b + 1, h:h + 1].float(),
+                                             v[b:b + 1, h:h + 1].float(), attn_mask=vis, scale=0.125)
+        worst = max(worst, (o[b:b + 1, h:h + 1].float() - ref).abs().max().item())
+    if worst > 2e-3:
+        raise SystemExit(f"parity gate failed ({worst}): no performance report")
+    for _ in range(args.warmup):
+        ext.fa_fwd_kv(q, k, v, causal, 0.125, coff)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        ext.fa_fwd_kv(q, k, v, causal, 0.125, coff)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    visible = Sq * (Sk - Sq) + Sq * (Sq + 1) // 2 if causal else Sq * Sk
+    flops = 4 * B * H * 64 * visible
+    kv_bytes = 2 * B * H * Sk * 64 * 2
+    io_bytes = kv_bytes + 2 * B * H * Sq * 64 * 2 + B * H * Sq * 4
+    tflops, gbs = flops / (ms / 1e3) / 1e12, io_bytes / (ms / 1e3) / 1e9
+    hbm = Sq == 1
+    return {
+        "metric": "decode attention GB/s (K, V, q read, O, LSE written)" if hbm
+                  else "KV-cache prefill-chunk attention forward TFLOP/s",
+        "value": round(gbs if hbm else tflops, 2), "unit": "GB/s" if hbm else "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"{args.config}: B={B} H={H} S_q={Sq} S_k={Sk} D=64 fp16, "
+                               + ("bottom-right causal" if causal else "all keys visible"),
+                   "B": B, "H": H, "S_q": Sq, "S_k": Sk, "causal_offset": coff},
+        "roofline": {"bound": "hbm" if hbm else "mfma", "achieved": round(gbs if hbm else tflops, 1),
+                     "peak": HBM_GBS if hbm else round(PEAK_TFLOPS, 1), "unit": "GB/s" if hbm else "TFLOP/s",
+                     "frac": round((gbs / HBM_GBS) if hbm else (tflops / PEAK_TFLOPS), 4), "traffic": None},
+        "parity": {"o_maxabs": worst},
+    }
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -270,6 +326,9 @@ def main():
     ext = fa.extension()
     if args.config == "5":
         print(json.dumps(decoder_step(args, torch, fa)), flush=True)
+        return
+    if args.config in ("kv-chunk", "kv-decode"):
+        print(json.dumps(kv_forward(args, torch, fa)), flush=True)
         return
     key = cfg_key(args.config)
     cfg = wl.CONFIGS[key]
