@@ -74,6 +74,18 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
  * hf_template/modeling_universal_lm.py:149-153 with the masks of :228-251). */
 int fa2_fwd_kv_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, void *stream);
 
+/* fa2_fwd_kv_f16 with the key range cut into nsplit slices of equal whole
+ * 64-key tiles, run as nsplit times as many workgroups, whose partial results
+ * (O accumulator, max, row sum per query) a second kernel merges -- for shapes
+ * with too few query blocks to fill the GPU (decode, short chunks).  Needs
+ * fa2_fwd_kv_workspace_bytes(B, H, S, nsplit) bytes of workspace, 16-byte
+ * aligned; nsplit = 1 is fa2_fwd_kv_f16 and needs none.  1 <= nsplit <= 1024.
+ * Same results as fa2_fwd_kv_f16 up to fp32 rounding of the merge.
+ * No counterpart in the reference (see fa2_fwd_kv_f16). */
+size_t fa2_fwd_kv_workspace_bytes(int32_t B, int32_t H, int32_t S, int32_t nsplit);
+int fa2_fwd_kv_split_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, int32_t nsplit,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
 /* Backward: dQ, dK, dV from Q, K, V, O, LSE and dO, recomputing P from LSE.
  * Replaces fav100::fa_bwd and its three kernels (delta, dQ, dK/dV)
  *   (reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:42-506).

@@ -56,12 +56,32 @@ def check(name, o, lse, q, k, v, causal, coff, scale=0.125):
     (100, 333, False, 0),      # non-causal, non-square
     (200, 129, True, 5),       # an offset that is no multiple of the tiles
 ])
-def test_kv_forward_vs_oracle(fa, Sq, Sk, causal, coff):
-    say(f"case kv Sq={Sq} Sk={Sk} causal={causal} offset={coff}")
+@pytest.mark.parametrize("nsplit", [1, 3, 0])
+def test_kv_forward_vs_oracle(fa, Sq, Sk, causal, coff, nsplit):
+    """nsplit 1: one pass; 3: three key slices merged; 0: the binding's automatic choice."""
+    say(f"case kv Sq={Sq} Sk={Sk} causal={causal} offset={coff} nsplit={nsplit}")
     q, k, v = inputs(2, 3, Sq, Sk, seed=Sq * 7 + Sk)
-    o, lse = fa.extension().fa_fwd_kv(q, k, v, causal, 0.125, coff)
+    o, lse = fa.extension().fa_fwd_kv(q, k, v, causal, 0.125, coff, nsplit)
     torch.cuda.synchronize()
-    check(f"kv Sq={Sq} Sk={Sk} c={causal} off={coff}", o, lse, q, k, v, causal, coff)
+    check(f"kv Sq={Sq} Sk={Sk} c={causal} off={coff} split={nsplit}", o, lse, q, k, v, causal, coff)
+
+
+@pytest.mark.parametrize("nsplit", [2, 5, 16, 40])
+def test_kv_split_matches_single_pass(fa, nsplit):
+    """Slices merged agree with one pass to rounding (O to fp16, LSE to a few fp32 ulps of values
+    up to ~20, summed in another order), also with more slices than the causal range of some query
+    blocks reaches and with empty trailing slices (40 > 26 tiles)."""
+    say(f"case kv split={nsplit} vs single pass")
+    q, k, v = inputs(2, 2, 300, 1650, seed=nsplit)
+    ext = fa.extension()
+    for causal, coff in ((True, 1350), (True, 0), (False, 0)):
+        o1, l1 = ext.fa_fwd_kv(q, k, v, causal, 0.125, coff, 1)
+        o2, l2 = ext.fa_fwd_kv(q, k, v, causal, 0.125, coff, nsplit)
+        torch.cuda.synchronize()
+        eo = (o1.float() - o2.float()).abs().max().item()
+        el = (l1 - l2).abs().max().item()
+        say(f"split {nsplit} causal={causal} off={coff}: O {eo:.2e} LSE {el:.2e}")
+        assert eo <= 2e-3 and el <= 5e-4
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -69,7 +89,7 @@ def test_kv_square_is_fa_fwd_bitwise(fa, causal):
     say(f"case kv square causal={causal}")
     q, k, v = inputs(2, 2, 333, 333, seed=5)
     ext = fa.extension()
-    o1, l1 = ext.fa_fwd_kv(q, k, v, causal, 0.125, 0)
+    o1, l1 = ext.fa_fwd_kv(q, k, v, causal, 0.125, 0, 1)     # one pass (no key slices)
     o2, l2 = ext.fa_fwd(q, k, v, 0.0, causal, 0.125, 0)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
@@ -108,6 +128,30 @@ def test_sdpa_routes_inference_shapes(fa):
     out = fa.sdpa(q, k, v, is_causal=False)       # needs a gradient: SDPA path, differentiable
     out.float().sum().backward()
     assert q.grad is not None
+
+
+def test_capi_kv_split_entry_point(fa):
+    """fa2_fwd_kv_split_f16 through ctypes, on a NaN-filled workspace (every partial it reads must
+    be written), equals the binding with the same nsplit."""
+    say("case C ABI fa2_fwd_kv_split_f16")
+    lib = capi.load()
+    q, k, v = inputs(1, 3, 1, 900, seed=4)
+    B, H, Sq, _ = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, Sq, device=DEV)
+    p = capi.fwd_params(q, k, v, o, lse, 0.125, causal=False)
+    nbytes = lib.fa2_fwd_kv_workspace_bytes(B, H, Sq, 7)
+    assert nbytes == 7 * B * H * Sq * 66 * 4
+    ws = torch.full((nbytes // 4,), float("nan"), device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.fa2_fwd_kv_split_f16(ctypes.byref(p), 900, 0, 7, ws.data_ptr(), nbytes, stream) == 0, \
+        lib.fa2_last_error()
+    assert lib.fa2_fwd_kv_split_f16(ctypes.byref(p), 900, 0, 7, ws.data_ptr(), nbytes - 4, stream) == 5
+    torch.cuda.synchronize()
+    o2, l2 = fa.extension().fa_fwd_kv(q, k, v, False, 0.125, 0, 7)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, l2)
+    check("capi split", o, lse, q, k, v, False, 0)
 
 
 def test_capi_kv_entry_point(fa):

@@ -88,6 +88,16 @@ def test_fwd_kv_validation_rejects_before_launch(s_k, coff, status):
     assert lib.fa2_fwd_kv_f16(ctypes.byref(p), 1 << 28, 0, None) == 2
 
 
+def test_fwd_kv_split_validation():
+    lib = capi.load()
+    assert lib.fa2_fwd_kv_workspace_bytes(2, 3, 5, 4) == 4 * 2 * 3 * 5 * 66 * 4
+    assert lib.fa2_fwd_kv_workspace_bytes(2, 3, 5, 1) == 0
+    p = _dummy_fwd()
+    for nsplit, status in ((0, 4), (1025, 4), (4, 5)):   # bad counts; nsplit > 1 without a workspace
+        rc = lib.fa2_fwd_kv_split_f16(ctypes.byref(p), 64, 0, nsplit, None, 0, None)
+        assert rc == status, (nsplit, rc, lib.fa2_last_error())
+
+
 def test_empty_problem_is_a_noop():
     lib = capi.load()
     for dim in ("B", "H", "S"):

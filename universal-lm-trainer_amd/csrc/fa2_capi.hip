@@ -92,10 +92,23 @@ const char *fa2_last_error(void) { return g_err; }
 
 const char *fa2_version(void) { return "fa2_mi355x 0.1 (gfx950, fp16 MFMA 32x32x16)"; }
 
+static size_t kv_part_bytes(int32_t B, int32_t H, int32_t S, int32_t nsplit) {
+    return (size_t)nsplit * B * H * S * (FA2_HEAD_DIM + 2) * sizeof(float);
+}
+
+size_t fa2_fwd_kv_workspace_bytes(int32_t B, int32_t H, int32_t S, int32_t nsplit) {
+    if (B <= 0 || H <= 0 || S <= 0 || nsplit <= 1) return 0;
+    return kv_part_bytes(B, H, S, nsplit);
+}
+
 // The forward over s_k key rows with key j visible to query i iff
-// j <= i + coff (causal); fa2_fwd_f16 is s_k = S, coff = 0.
-static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *stream) {
+// j <= i + coff (causal); fa2_fwd_f16 is s_k = S, coff = 0.  nsplit > 1
+// cuts the key range into slices whose partial results (in the workspace)
+// a second kernel merges.
+static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *stream, int32_t nsplit = 1,
+                      void *workspace = nullptr, size_t workspace_bytes = 0) {
     if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
+    if (nsplit < 1 || nsplit > 1024) return fail(FA2_ERR_BAD_ARGUMENT, "nsplit %d outside 1..1024", nsplit);
     int rc = check_shape(p->B, p->H, p->S, p->D, 256);
     if (rc) return rc;
     if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
@@ -104,6 +117,13 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
         return fail(FA2_ERR_BAD_SHAPE, "key length %d outside 1 .. 2^31 / (B*H)", s_k);
     if (coff < -(1 << 30) || coff > (1 << 30))
         return fail(FA2_ERR_BAD_ARGUMENT, "causal offset %d outside +-2^30", coff);
+    if (nsplit > 1) {
+        const size_t need = kv_part_bytes(p->B, p->H, p->S, nsplit);
+        if (!workspace || workspace_bytes < need)
+            return fail(FA2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : 0);
+        if (reinterpret_cast<uintptr_t>(workspace) & 15u)
+            return fail(FA2_ERR_MISALIGNED, "workspace is not 16-byte aligned");
+    }
     if ((rc = check_tensor("q", p->q, p->q_stride, p->B, p->H, p->S, true))) return rc;
     if ((rc = check_tensor("k", p->k, p->k_stride, p->B, p->H, s_k, true))) return rc;
     if ((rc = check_tensor("v", p->v, p->v_stride, p->B, p->H, s_k, true))) return rc;
@@ -128,12 +148,18 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     a.B = p->B; a.H = p->H; a.S = p->S;
     a.Sk = s_k;
     a.coff = coff;
+    const int32_t tiles = (s_k + 63) / 64;
+    a.nsplit = nsplit;
+    a.split_keys = 64 * ((tiles + nsplit - 1) / nsplit);
+    a.part_o = static_cast<float *>(workspace);
+    a.part_ml = nsplit > 1 ? a.part_o + (size_t)nsplit * p->B * p->H * p->S * FA2_HEAD_DIM : nullptr;
     a.scale2 = scale2_of(p->softmax_scale);
     a.negate = p->softmax_scale < 0.f;
     a.seed = p->seed;
     a.drop_thr = drop_threshold(p->dropout_p);
     a.inv_keep = 1.f / (1.f - p->dropout_p);
-    const hipError_t e = fa2::launch_fwd(a, p->causal != 0, p->dropout_p > 0.f, (hipStream_t)stream);
+    const hipError_t e = nsplit > 1 ? fa2::launch_fwd_split(a, p->causal != 0, p->dropout_p > 0.f, (hipStream_t)stream)
+                                    : fa2::launch_fwd(a, p->causal != 0, p->dropout_p > 0.f, (hipStream_t)stream);
     if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "forward launch: %s", hipGetErrorString(e));
     return FA2_OK;
 }
@@ -146,6 +172,12 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
 int fa2_fwd_kv_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, void *stream) {
     g_err[0] = 0;
     return fwd_common(p, s_k, causal_offset, stream);
+}
+
+int fa2_fwd_kv_split_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, int32_t nsplit,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    return fwd_common(p, s_k, causal_offset, stream, nsplit, workspace, workspace_bytes);
 }
 
 // Workspace: fp32 delta and log2-scaled LSE, [B*H*S] each (rounded up to 256

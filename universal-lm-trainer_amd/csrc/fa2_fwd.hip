@@ -57,7 +57,11 @@ constexpr int QWG = NW * 32 * QB;  // queries per workgroup
 constexpr int NST = FA2_FWD_NST;   // LDS stages of (K, V) tiles: 4 or 5
 constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <= 2^15
 
-template <bool CAUSAL, bool DROPOUT>
+// SPLIT: the key range is cut into a.nsplit slices of a.split_keys keys; the
+// workgroup of slice ks runs the same pipeline over its slice and writes the
+// unnormalised partial result (O accumulator, reference max, row sum) for
+// fwd_combine_kernel instead of O and LSE.
+template <bool CAUSAL, bool DROPOUT, bool SPLIT>
 __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs a) {
     // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
     __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
@@ -70,9 +74,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     const int coff = a.coff; // causal: key j visible to query i iff j <= i + coff
     const int BH = a.B * a.H;
     const int nqblk = (S + QWG - 1) / QWG;
-    const int L = blockIdx.x;
-    const int qblk = nqblk - 1 - L / BH;
-    const int bh = L - (L / BH) * BH;
+    const int nsplit = SPLIT ? a.nsplit : 1;
+    const int L = blockIdx.x;                          // (query block, slice, b*H + h), heads fastest
+    const int qslot = L / (BH * nsplit);
+    const int qblk = nqblk - 1 - qslot;                // heaviest (last) query blocks first
+    const int rem = L - qslot * (BH * nsplit);
+    const int ks = SPLIT ? rem / BH : 0;
+    const int bh = rem - ks * BH;
     const int b = bh / a.H, h = bh - b * a.H;
 
     const _Float16 *Qp = a.q + b * a.qsb + h * a.qsh;
@@ -85,15 +93,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     const int qw0 = q_wg0 + wave * 32 * QB;   // this wave's queries: qw0 .. qw0 + 32*QB - 1
     const float scale2 = a.scale2;
 
-    const int kend = CAUSAL ? min(Sk, q_wg0 + QWG + coff) : Sk;
-    const int ntiles = kend > 0 ? (kend + KT - 1) / KT : 0;
+    // Keys kbase .. kend-1, in tiles t = 0 .. ntiles-1 starting at key kbase.
+    const int kbase = SPLIT ? ks * a.split_keys : 0;   // split_keys: a multiple of KT
+    const int kend_wg = CAUSAL ? min(Sk, q_wg0 + QWG + coff) : Sk;
+    const int kend = SPLIT ? min(kend_wg, kbase + a.split_keys) : kend_wg;
+    const int ntiles = kend > kbase ? (kend - kbase + KT - 1) / KT : 0;
     // Last key tile this wave computes (-1: none).  Every wave still joins
     // every barrier and moves its share of every tile.
-    const int kw_end = CAUSAL ? min(qw0 + 32 * QB + coff, Sk) : Sk;   // keys the wave's queries reach
-    const int tlast = (qw0 >= S || kw_end <= 0) ? -1 : (kw_end - 1) / KT;
+    const int kw_end = min(CAUSAL ? min(qw0 + 32 * QB + coff, Sk) : Sk, kend);   // keys the wave's queries reach
+    const int tlast = (qw0 >= S || kw_end <= kbase) ? -1 : (kw_end - 1 - kbase) / KT;
     // Tiles before tsteady are visible to every query of the wave (the
     // steady, mask-free path); the rest run the general path.
-    const int tsteady = CAUSAL ? min(tlast, max(qw0 + coff + 1, 0) / KT) : tlast;
+    const int tsteady = CAUSAL ? min(tlast, max(qw0 + coff + 1 - kbase, 0) / KT) : tlast;
 
     // Q^T operand of d-step st: lane holds Q[q][16*st + 8*g2 + e].  Rows past
     // S load row S - 1 (unconditional loads stay in flight together); those
@@ -136,9 +147,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // Tiles are issued in order, once each: scalar running addresses (global
     // tile bases, LDS stage) advance by a constant per tile instead of being
     // recomputed with 64-bit multiplies at every transfer.
-    uint64_t gk = (uint64_t)(uintptr_t)Kp, gv = (uint64_t)(uintptr_t)Vp;
+    uint64_t gk = (uint64_t)(uintptr_t)(Kp + (int64_t)kbase * a.kss);
+    uint64_t gv = (uint64_t)(uintptr_t)(Vp + (int64_t)kbase * a.vss);
     const uint64_t k_step = (uint64_t)KT * a.kss * 2, v_step = (uint64_t)KT * a.vss * 2;
-    int kn = 0;          // first key of the next tile to issue
+    int kn = kbase;      // first key of the next tile to issue
     uint32_t stn = 0;    // its stage
     const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 1024u * (uint32_t)(TPW * wave);
     auto issue = [&](int) FA2_INLINE {
@@ -393,14 +405,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         float rs[QB];
         step(stage_of(t + 1), stage_of(t + NST - 1), s_nxt, p_prv, s_cur, p_cur, rs);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) softmax_tail(qb, t * KT, stage_of(t), p_cur[qb], rs[qb]);
+        for (int qb = 0; qb < QB; ++qb) softmax_tail(qb, kbase + t * KT, stage_of(t), p_cur[qb], rs[qb]);
         tile_end(t);
     };
     // First tile, this wave's last (diagonal / tail) tile, and the tiles after
     // it, where the wave only drains PV and keeps moving its share of tiles.
     auto general = [&](int t, f16x(&s_cur)[QB][2], h8(&p_cur)[QB][2][2], f16x(&s_nxt)[QB][2],
                        h8(&p_prv)[QB][2][2]) FA2_INLINE {
-        const int k0 = t * KT;
+        const int k0 = kbase + t * KT;
         if (t >= 1 && t - 1 <= tlast) pv(stage_of(t + NST - 1), p_prv);
         if (t <= tlast) {
             // Serial order (rare path): each operand dies before the next
@@ -453,6 +465,30 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         if (t + 1 < ntiles) general(t + 1, s1, p1, s0, p0);
     }
 
+    if (SPLIT) {
+        // Partial result of this slice: the O^T accumulator, the reference
+        // max and the row sum (all relative to 2^msc), for the combine step.
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const float lt = l[qb] + xor32(l[qb]);
+            const int q = qw0 + 32 * qb + c;
+            if (q < S) {
+                const int64_t row = ((int64_t)ks * BH + bh) * S + q;
+                float *po = a.part_o + row * HD;
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        f4 x;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j];
+                        *reinterpret_cast<f4 *>(po + 32 * db + 8 * i + 4 * g2) = x;
+                    }
+                if (g2 == 0) *reinterpret_cast<f2 *>(a.part_ml + 2 * row) = f2{msc[qb], lt};
+            }
+        }
+        return;
+    }
     // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -475,23 +511,73 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     }
 }
 
-}  // namespace
+// Merges the slices of a split forward: with M the largest reference max of
+// a query's slices and w_s = 2^(m_s - M), O = sum_s w_s O_s / sum_s w_s l_s
+// and LSE = (M + log2 sum_s w_s l_s) ln 2 (a query no slice saw: O = 0,
+// LSE = -inf).  16 threads per query, 4 of its 64 columns each.
+__global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdArgs a) {
+    const int S = a.S;
+    const int64_t BHS = (int64_t)a.B * a.H * S;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);   // (b*H + h)*S + q
+    if (row >= BHS) return;
+    const int part = threadIdx.x & 15;
+    const int bh = (int)(row / S), q = (int)(row - (int64_t)bh * S);
+    const int b = bh / a.H, h = bh - b * a.H;
+    float M = -INFINITY;
+    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[2 * (s * BHS + row)]);
+    float lsum = 0.f;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
+        for (int s = 0; s < a.nsplit; ++s) {
+            const f2 ml = *reinterpret_cast<const f2 *>(a.part_ml + 2 * (s * BHS + row));
+            if (ml[0] == -INFINITY) continue;
+            const float w = __builtin_amdgcn_exp2f(ml[0] - M);
+            lsum += w * ml[1];
+            const f4 x = *reinterpret_cast<const f4 *>(a.part_o + (s * BHS + row) * HD + 4 * part);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] += w * x[j];
+        }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] *= inv;
+    *reinterpret_cast<h4 *>(a.o + b * a.osb + h * a.osh + (int64_t)q * a.oss + 4 * part) =
+        __builtin_convertvector(acc, h4);
+    if (part == 0)
+        a.lse[b * a.lsb + h * a.lsh + q] = (M == -INFINITY || !(lsum > 0.f)) ? -INFINITY : (M + log2f(lsum)) * LN2;
+}
 
-hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+template <bool SPLIT>
+void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const int nqblk = (a.S + QWG - 1) / QWG;
-    const dim3 grid((unsigned)(nqblk * a.B * a.H));
+    const dim3 grid((unsigned)(nqblk * a.B * a.H * (SPLIT ? a.nsplit : 1)));
     const dim3 block(NW * 64);
     if (causal) {
         if (dropout)
-            hipLaunchKernelGGL((fwd_kernel<true, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((fwd_kernel<true, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<true, false, SPLIT>), grid, block, 0, st, a);
     } else {
         if (dropout)
-            hipLaunchKernelGGL((fwd_kernel<false, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((fwd_kernel<false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<false, false, SPLIT>), grid, block, 0, st, a);
     }
+}
+
+}  // namespace
+
+hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    launch_fwd_t<false>(a, causal, dropout, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd_split(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    launch_fwd_t<true>(a, causal, dropout, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t rows = (int64_t)a.B * a.H * a.S;
+    hipLaunchKernelGGL(fwd_combine_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -18,6 +18,12 @@ struct FwdArgs {
     int B, H, S;         // S: query rows (q, o, lse)
     int Sk;              // key / value rows
     int coff;            // causal: key j visible to query i iff j <= i + coff
+    // Split forward (launch_fwd_split): nsplit slices of split_keys keys (a
+    // multiple of 64); partials [nsplit, B*H, S] x (64 fp32 O) and x (max, sum).
+    int nsplit;
+    int split_keys;
+    float *part_o;
+    float *part_ml;
     float scale2;        // |softmax_scale| * log2(e), at least FLT_MIN
     int negate;          // softmax_scale < 0: the Q operand is negated
     uint32_t seed;       // dropout hash seed
@@ -61,6 +67,8 @@ struct RopeArgs {
 
 // Launchers; each returns the hipError_t of its launch.
 hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st);
+// The forward over a.nsplit key slices (partials into a.part_o / a.part_ml), then their merge.
+hipError_t launch_fwd_split(const FwdArgs &a, bool causal, bool dropout, hipStream_t st);
 hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);
 hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);

@@ -4,9 +4,10 @@
 // output conventions (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:386-397):
 //   fa_fwd(q, k, v, dropout_p, causal, softmax_scale, seed)            -> [o, lse]
 // plus, for inference callers (no reference counterpart; fa2_fwd_kv_f16):
-//   fa_fwd_kv(q, k, v, causal, softmax_scale, causal_offset)           -> [o, lse]
+//   fa_fwd_kv(q, k, v, causal, softmax_scale, causal_offset, nsplit=0)  -> [o, lse]
 // with k, v of their own sequence length and key j visible to query i iff
-// j <= i + causal_offset when causal.
+// j <= i + causal_offset when causal; nsplit slices of the key range
+// (fa2_fwd_kv_split_f16, 0 = chosen here so the grid fills the GPU).
 //   fa_bwd(q, k, v, o, lse, do, dropout_p, causal, softmax_scale, seed,
 //          mode=7)                                                      -> [dq, dk, dv]
 //   rope_fwd(q, k, cos, sin)                                            -> [qo, ko]
@@ -21,6 +22,7 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "../../include/fa2_mi355x.h"
@@ -56,7 +58,7 @@ void check_qkv(const torch::Tensor &q, const torch::Tensor &k, const torch::Tens
 // The forward through fa2_fwd_kv_f16 (s_k = k's length); fa_fwd is the square case.
 std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor &k, const torch::Tensor &v,
                                     double dropout_p, bool causal, double softmax_scale, int64_t seed,
-                                    int64_t causal_offset, const char *op) {
+                                    int64_t causal_offset, const char *op, int64_t nsplit = 1) {
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     const int64_t B = q.size(0), H = q.size(1), S = q.size(2);
     // O follows q's memory order the way an eager elementwise output would:
@@ -92,7 +94,15 @@ std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor 
     p.causal = causal ? 1 : 0;
     TORCH_CHECK(k.size(2) <= INT32_MAX && causal_offset >= INT32_MIN && causal_offset <= INT32_MAX,
                 op, ": key length / causal offset out of range");
-    check_status(fa2_fwd_kv_f16(&p, (int32_t)k.size(2), (int32_t)causal_offset, current_stream(q)), op);
+    if (nsplit <= 1) {
+        check_status(fa2_fwd_kv_f16(&p, (int32_t)k.size(2), (int32_t)causal_offset, current_stream(q)), op);
+    } else {
+        const size_t bytes = fa2_fwd_kv_workspace_bytes(p.B, p.H, p.S, (int32_t)nsplit);
+        auto ws = torch::empty({(int64_t)(bytes / 4) + 4}, q.options().dtype(torch::kFloat));
+        check_status(fa2_fwd_kv_split_f16(&p, (int32_t)k.size(2), (int32_t)causal_offset, (int32_t)nsplit,
+                                          ws.data_ptr(), ws.numel() * 4, current_stream(q)),
+                     op);
+    }
     return {o, lse};
 }
 
@@ -102,8 +112,16 @@ std::vector<torch::Tensor> fa_fwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     return fwd_impl(q, k, v, dropout_p, causal, softmax_scale, seed, 0, "fa_fwd");
 }
 
+// Key slices for a grid of `wgs` workgroups over `tiles` 64-key tiles: about
+// 384 workgroups in all (1.5 per CU) with at least 8 tiles per slice -- the
+// best of a sweep over decode (S_q = 1, S_k = 4K..16K, B*H = 12..96) and
+// chunks (S_q = 128..512); more slices lose to each slice's fixed costs.
+int64_t auto_nsplit(int64_t wgs, int64_t tiles) {
+    return std::max<int64_t>(1, std::min<int64_t>(384 / wgs, tiles / 8));
+}
+
 std::vector<torch::Tensor> fa_fwd_kv(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal,
-                                     double softmax_scale, int64_t causal_offset) {
+                                     double softmax_scale, int64_t causal_offset, int64_t nsplit) {
     TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "inputs must be on the GPU");
     TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
                 "only fp16 supported");
@@ -114,7 +132,9 @@ std::vector<torch::Tensor> fa_fwd_kv(torch::Tensor q, torch::Tensor k, torch::Te
     TORCH_CHECK(k.size(2) >= 1, "empty key sequence");
     TORCH_CHECK(k.device() == q.device() && v.device() == q.device(), "q/k/v device mismatch");
     TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1, "last dim must be contiguous");
-    return fwd_impl(q, k, v, 0.0, causal, softmax_scale, 0, causal_offset, "fa_fwd_kv");
+    TORCH_CHECK(nsplit >= 0 && nsplit <= 1024, "nsplit must be 0 (automatic) .. 1024");
+    if (nsplit == 0) nsplit = auto_nsplit((q.size(2) + 127) / 128 * q.size(0) * q.size(1), (k.size(2) + 63) / 64);
+    return fwd_impl(q, k, v, 0.0, causal, softmax_scale, 0, causal_offset, "fa_fwd_kv", nsplit);
 }
 
 std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor o,
@@ -263,7 +283,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("fa_fwd", &fa_fwd, "FA2 forward (gfx950 MFMA)");
     m.def("fa_fwd_kv", &fa_fwd_kv, "FA2 forward, k/v of their own length (inference)", pybind11::arg("q"),
           pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("causal"), pybind11::arg("softmax_scale"),
-          pybind11::arg("causal_offset"));
+          pybind11::arg("causal_offset"), pybind11::arg("nsplit") = 0);
     m.def("fa_bwd", &fa_bwd, "FA2 backward (gfx950 MFMA)", pybind11::arg("q"), pybind11::arg("k"),
           pybind11::arg("v"), pybind11::arg("o"), pybind11::arg("lse"), pybind11::arg("do"),
           pybind11::arg("dropout_p"), pybind11::arg("causal"), pybind11::arg("softmax_scale"),

@@ -74,6 +74,11 @@ def load():
         lib.fa2_fwd_f16.restype = ctypes.c_int
         lib.fa2_fwd_kv_f16.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
         lib.fa2_fwd_kv_f16.restype = ctypes.c_int
+        lib.fa2_fwd_kv_split_f16.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_int32, ctypes.c_int32,
+                                             ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.fa2_fwd_kv_split_f16.restype = ctypes.c_int
+        lib.fa2_fwd_kv_workspace_bytes.argtypes = [ctypes.c_int32] * 4
+        lib.fa2_fwd_kv_workspace_bytes.restype = ctypes.c_size_t
         lib.fa2_bwd_f16.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int32, ctypes.c_void_p,
                                     ctypes.c_size_t, ctypes.c_void_p]
         lib.fa2_bwd_f16.restype = ctypes.c_int
