@@ -68,7 +68,8 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
  * j <= i + causal_offset: 0 is torch SDPA's is_causal alignment (top-left),
  * s_k - S the KV-cache one (bottom-right: the chunk is the last S positions).
  * A query that sees no key gets O = 0 and LSE = -inf.  s_k = S with
- * causal_offset = 0 is fa2_fwd_f16, bit for bit.
+ * causal_offset = 0 is fa2_fwd_f16, bit for bit, except for S = 1 without
+ * dropout (decode), which takes a kernel of its own (equal to rounding).
  * No counterpart in the reference, whose kernel is square-only: its inference
  * paths call torch SDPA on exactly these shapes (reference @ None: inf.py:128-133,
  * hf_template/modeling_universal_lm.py:149-153 with the masks of :228-251). */

@@ -105,8 +105,10 @@ size_t fa2_fwd_kv_workspace_bytes(int32_t B, int32_t H, int32_t S, int32_t nspli
 // j <= i + coff (causal); fa2_fwd_f16 is s_k = S, coff = 0.  nsplit > 1
 // cuts the key range into slices whose partial results (in the workspace)
 // a second kernel merges.
-static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *stream, int32_t nsplit = 1,
-                      void *workspace = nullptr, size_t workspace_bytes = 0) {
+// `inference`: the fa2_fwd_kv_* entry points, where one query without dropout
+// takes the decode kernel.
+static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *stream, bool inference,
+                      int32_t nsplit = 1, void *workspace = nullptr, size_t workspace_bytes = 0) {
     if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
     if (nsplit < 1 || nsplit > 1024) return fail(FA2_ERR_BAD_ARGUMENT, "nsplit %d outside 1..1024", nsplit);
     int rc = check_shape(p->B, p->H, p->S, p->D, 256);
@@ -151,33 +153,36 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     const int32_t tiles = (s_k + 63) / 64;
     a.nsplit = nsplit;
     a.split_keys = 64 * ((tiles + nsplit - 1) / nsplit);
-    a.part_o = static_cast<float *>(workspace);
+    a.part_o = nsplit > 1 ? static_cast<float *>(workspace) : nullptr;
     a.part_ml = nsplit > 1 ? a.part_o + (size_t)nsplit * p->B * p->H * p->S * FA2_HEAD_DIM : nullptr;
     a.scale2 = scale2_of(p->softmax_scale);
     a.negate = p->softmax_scale < 0.f;
     a.seed = p->seed;
     a.drop_thr = drop_threshold(p->dropout_p);
     a.inv_keep = 1.f / (1.f - p->dropout_p);
-    const hipError_t e = nsplit > 1 ? fa2::launch_fwd_split(a, p->causal != 0, p->dropout_p > 0.f, (hipStream_t)stream)
-                                    : fa2::launch_fwd(a, p->causal != 0, p->dropout_p > 0.f, (hipStream_t)stream);
+    const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
+    const hipStream_t st = (hipStream_t)stream;
+    const hipError_t e = (inference && p->S == 1 && !dropout) ? fa2::launch_fwd_decode(a, causal, st)
+                         : nsplit > 1                         ? fa2::launch_fwd_split(a, causal, dropout, st)
+                                                              : fa2::launch_fwd(a, causal, dropout, st);
     if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "forward launch: %s", hipGetErrorString(e));
     return FA2_OK;
 }
 
 int fa2_fwd_f16(const fa2_fwd_params *p, void *stream) {
     g_err[0] = 0;
-    return fwd_common(p, p ? p->S : 0, 0, stream);
+    return fwd_common(p, p ? p->S : 0, 0, stream, false);
 }
 
 int fa2_fwd_kv_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, void *stream) {
     g_err[0] = 0;
-    return fwd_common(p, s_k, causal_offset, stream);
+    return fwd_common(p, s_k, causal_offset, stream, true);
 }
 
 int fa2_fwd_kv_split_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, int32_t nsplit,
                          void *workspace, size_t workspace_bytes, void *stream) {
     g_err[0] = 0;
-    return fwd_common(p, s_k, causal_offset, stream, nsplit, workspace, workspace_bytes);
+    return fwd_common(p, s_k, causal_offset, stream, true, nsplit, workspace, workspace_bytes);
 }
 
 // Workspace: fp32 delta and log2-scaled LSE, [B*H*S] each (rounded up to 256

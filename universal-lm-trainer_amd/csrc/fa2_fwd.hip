@@ -547,6 +547,154 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdArgs a) {
         a.lse[b * a.lsb + h * a.lsh + q] = (M == -INFINITY || !(lsum > 0.f)) ? -INFINITY : (M + log2f(lsum)) * LN2;
 }
 
+// ---------------------------------------------------------------------------
+// Decode: one query against Sk keys.  VALU only -- the work is streaming K and
+// V from HBM once; an MFMA tile would use one of its 32 query rows.
+// ---------------------------------------------------------------------------
+// Workgroup (slice ks, b*H + h) takes the keys of slice ks (all keys when
+// nsplit = 1), cut into four runs of whole 64-key blocks, one per wave.  Per
+// block, lane L = 8g + c8 loads the 16-byte chunk c8 (dims 8*c8 .. +7) of key
+// rows k0 + 8i + g, i = 0..7, of K and of V (each of the eight loads covers 1 KB
+// of consecutive rows), forms the partial dot of its chunk with q's, and a
+// butterfly over the 8 lanes of group g gives all of them the score of row
+// 8i + g.  Each lane runs the online softmax over its rows {8i + g} and
+// accumulates P V for its 8 dims.  The groups' states merge by shuffles (lanes
+// xor 8, 16, 32), the waves' in LDS; the result is O and LSE (nsplit = 1) or
+// the slice's partial for fwd_combine_kernel.
+constexpr int DEC_NW = 4;
+
+// Sum over the 8 lanes of each aligned group of 8, returned to all of them:
+// DPP quad_perm [1,0,3,2] and [2,3,0,1] (partners xor 1, xor 2), then
+// row_half_mirror (lane i <-> 7 - i of each 8, which lies in the other quad).
+__device__ __forceinline__ float sum8(float x) {
+    x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
+    return x;
+}
+
+__device__ __forceinline__ void merge_state(float &m, float &l, f8 &acc, float mo, float lo, const f8 &ao) {
+    const float mx = fmaxf(m, mo);
+    const float wa = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+    const float wb = (mo == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mo - mx);
+    l = l * wa + lo * wb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = acc[e] * wa + ao[e] * wb;
+    m = mx;
+}
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(DEC_NW * 64) void decode_kernel(const FwdArgs a) {
+    __shared__ float sm[DEC_NW][HD + 2];   // per wave: O accumulator, max, sum
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 3, c8 = lane & 7;
+    const int BH = a.B * a.H;
+    const int ks = blockIdx.x / BH, bh = blockIdx.x - ks * BH;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int Sk = a.Sk;
+    const int kend = CAUSAL ? min(Sk, a.coff + 1) : Sk;   // query 0 sees keys j <= coff
+    const int kb = ks * a.split_keys, ke = min(kend, kb + a.split_keys);
+    const int nblk = ke > kb ? (ke - kb + 63) / 64 : 0;
+    const int per = (nblk + DEC_NW - 1) / DEC_NW;
+    const int wb = kb + 64 * min(nblk, wave * per);
+    const int we = min(ke, kb + 64 * min(nblk, (wave + 1) * per));
+    const _Float16 *Kp = a.k + b * a.ksb + h * a.ksh + 8 * c8;
+    const _Float16 *Vp = a.v + b * a.vsb + h * a.vsh + 8 * c8;
+    const h8 qv = *reinterpret_cast<const h8 *>(a.q + b * a.qsb + h * a.qsh + 8 * c8);
+    const h8 qn = a.negate ? neg_h8(qv) : qv;
+    const float scale2 = a.scale2;
+
+    float m = -INFINITY, l = 0.f;
+    f8 acc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    // Block k0's rows are loaded while block k0 - 64 is computed (two register sets).
+    h8 kn[8], vn[8];
+    auto load = [&](int k0) FA2_INLINE {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = min(k0 + 8 * i + g, Sk - 1);   // rows past the run: loaded in bounds, masked
+            kn[i] = *reinterpret_cast<const h8 *>(Kp + (int64_t)r * a.kss);
+            vn[i] = *reinterpret_cast<const h8 *>(Vp + (int64_t)r * a.vss);
+        }
+    };
+    if (wb < we) load(wb);
+    for (int k0 = wb; k0 < we; k0 += 64) {
+        h8 kx[8], vx[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            kx[i] = kn[i];
+            vx[i] = vn[i];
+        }
+        if (k0 + 64 < we) load(k0 + 64);
+        float s[8];
+        float mx = m;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const h2 qq = {qn[2 * e], qn[2 * e + 1]}, kk = {kx[i][2 * e], kx[i][2 * e + 1]};
+                d = __builtin_amdgcn_fdot2(qq, kk, d, false);
+            }
+            d = sum8(d);
+            s[i] = (k0 + 8 * i + g < we) ? d * scale2 : -INFINITY;
+            mx = fmaxf(mx, s[i]);
+        }
+        const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float p = (s[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s[i] - mx);
+            l += p;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] += p * (float)vx[i][e];
+        }
+        m = mx;
+    }
+    // Merge the 8 row groups (lanes with the same c8), then the waves.
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        f8 ao;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ao[e] = __shfl_xor(acc[e], off);
+        merge_state(m, l, acc, __shfl_xor(m, off), __shfl_xor(l, off), ao);
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm[wave][8 * c8 + e] = acc[e];
+        if (c8 == 0) {
+            sm[wave][HD] = m;
+            sm[wave][HD + 1] = l;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DEC_NW; ++w) M = fmaxf(M, sm[w][HD]);
+    float L = 0.f, o = 0.f;   // lane = dim
+    if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < DEC_NW; ++w) {
+            const float mw = sm[w][HD];
+            if (mw == -INFINITY) continue;
+            const float wt = __builtin_amdgcn_exp2f(mw - M);
+            L += wt * sm[w][HD + 1];
+            o += wt * sm[w][lane];
+        }
+    }
+    if (a.part_o) {   // slice partial: (ks * BH + bh) * S + q with S = 1, q = 0
+        const int64_t row = (int64_t)ks * BH + bh;
+        a.part_o[row * HD + lane] = o;
+        if (lane == 0) *reinterpret_cast<f2 *>(a.part_ml + 2 * row) = f2{M, L};
+        return;
+    }
+    a.o[b * a.osb + h * a.osh + lane] = (_Float16)(L > 0.f ? o / L : 0.f);
+    if (lane == 0) a.lse[b * a.lsb + h * a.lsh] = (M == -INFINITY || !(L > 0.f)) ? -INFINITY : (M + log2f(L)) * LN2;
+}
+
 template <bool SPLIT>
 void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const int nqblk = (a.S + QWG - 1) / QWG;
@@ -569,6 +717,18 @@ void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
 
 hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     launch_fwd_t<false>(a, causal, dropout, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd_decode(const FwdArgs &a, bool causal, hipStream_t st) {
+    const dim3 grid((unsigned)(a.B * a.H * a.nsplit)), block(DEC_NW * 64);
+    if (causal)
+        hipLaunchKernelGGL(decode_kernel<true>, grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL(decode_kernel<false>, grid, block, 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.nsplit <= 1) return e;
+    hipLaunchKernelGGL(fwd_combine_kernel, dim3((unsigned)((a.B * a.H + 15) / 16)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -69,6 +69,9 @@ struct RopeArgs {
 hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st);
 // The forward over a.nsplit key slices (partials into a.part_o / a.part_ml), then their merge.
 hipError_t launch_fwd_split(const FwdArgs &a, bool causal, bool dropout, hipStream_t st);
+// One query (S = 1), no dropout: the VALU decode kernel over a.nsplit slices
+// (a.part_o null when nsplit = 1), then the merge when nsplit > 1.
+hipError_t launch_fwd_decode(const FwdArgs &a, bool causal, hipStream_t st);
 hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);
 hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);

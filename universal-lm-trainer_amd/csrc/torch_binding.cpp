@@ -120,6 +120,13 @@ int64_t auto_nsplit(int64_t wgs, int64_t tiles) {
     return std::max<int64_t>(1, std::min<int64_t>(384 / wgs, tiles / 8));
 }
 
+// Decode (one query, the VALU kernel, four waves per workgroup each taking a
+// quarter of its slice): about 192 workgroups and at least 1024 keys per
+// slice -- the best of a sweep over B*H = 12..384 and S_k = 1K..16K.
+int64_t auto_nsplit_decode(int64_t bh, int64_t s_k) {
+    return std::max<int64_t>(1, std::min<int64_t>((192 + bh - 1) / bh, s_k / 1024));
+}
+
 std::vector<torch::Tensor> fa_fwd_kv(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal,
                                      double softmax_scale, int64_t causal_offset, int64_t nsplit) {
     TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "inputs must be on the GPU");
@@ -133,7 +140,9 @@ std::vector<torch::Tensor> fa_fwd_kv(torch::Tensor q, torch::Tensor k, torch::Te
     TORCH_CHECK(k.device() == q.device() && v.device() == q.device(), "q/k/v device mismatch");
     TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1, "last dim must be contiguous");
     TORCH_CHECK(nsplit >= 0 && nsplit <= 1024, "nsplit must be 0 (automatic) .. 1024");
-    if (nsplit == 0) nsplit = auto_nsplit((q.size(2) + 127) / 128 * q.size(0) * q.size(1), (k.size(2) + 63) / 64);
+    if (nsplit == 0)
+        nsplit = q.size(2) == 1 ? auto_nsplit_decode(q.size(0) * q.size(1), k.size(2))
+                                : auto_nsplit((q.size(2) + 127) / 128 * q.size(0) * q.size(1), (k.size(2) + 63) / 64);
     return fwd_impl(q, k, v, 0.0, causal, softmax_scale, 0, causal_offset, "fa_fwd_kv", nsplit);
 }
 
