@@ -423,7 +423,25 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
                     FA2_COLD_BRANCH();
                     mask(qb, k0, s_cur[qb]);
                 }
-                softmax_tail(qb, k0, stage_of(t), p_cur[qb], p_form(s_cur[qb], msc[qb], p_cur[qb]));
+                float rs;
+                if (t == 0) {
+                    // First tile: msc is -inf, so P against it would only
+                    // overflow into the cold path.  The scores are still
+                    // live here: take the row max from them directly (the
+                    // value the cold path would compute, -inf when every key
+                    // is masked).
+                    float mx = s_cur[qb][0][0];
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[qb][kb][r]);
+                    mx = fmaxf(mx, xor32(mx)) * scale2;
+                    msc[qb] = mx;
+                    rs = p_form(s_cur[qb], (mx == -INFINITY) ? 0.f : mx, p_cur[qb]);
+                } else {
+                    rs = p_form(s_cur[qb], msc[qb], p_cur[qb]);
+                }
+                softmax_tail(qb, k0, stage_of(t), p_cur[qb], rs);
             }
             if (t + 1 <= tlast) s_mm(stage_of(t + 1), s_nxt);
             if (t == ntiles - 1) pv(stage_of(t), p_cur);   // nothing after it drains P(t)
