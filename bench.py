@@ -395,6 +395,25 @@ def main():
     kernels = {kname: {"avg_ms": round(avg[kname], 4), "executed_gflop": round(executed[kname] / 1e9, 2),
                        "tflops": round(executed[kname] / (avg[kname] / 1e3) / 1e12, 1)} for kname in avg}
 
+    # Cold L2: each step preceded by a 512 MB buffer write (larger than the
+    # L2s and the MALL share a step touches), timed alone; median of 10.
+    flush = torch.empty(512 * 2**20 // 4, device=dev)
+    cold = []
+    for i in range(10):
+        flush.fill_(float(i))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cold.append(e0.elapsed_time(e1))
+    del flush
+    cold_ms = statistics.median(cold)
+    timing = {"fwd_ms": round(avg["fwd"], 4), "bwd_ms": round(avg["bwd_dq"] + avg["bwd_dkv"], 4),
+              "fwd_bwd_ms": round(sum(avg.values()), 4),
+              "cold_l2": {"ms_per_step": round(cold_ms, 4), "tflops": round(step_flops / (cold_ms / 1e3) / 1e12, 1),
+                          "flush_mb": 512, "sample": "median of 10 steps, each after a 512 MB device write"}}
+
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -416,6 +435,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": round(PEAK_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(dom)},
         "kernels": kernels,
+        "timing": timing,
         "parity": parity,
     }
     if not args.no_cpu:
