@@ -80,7 +80,8 @@ int fa2_fwd_kv_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_offset, 
  * (O accumulator, max, row sum per query) a second kernel merges -- for shapes
  * with too few query blocks to fill the GPU (decode, short chunks).  Needs
  * fa2_fwd_kv_workspace_bytes(B, H, S, nsplit) bytes of workspace, 16-byte
- * aligned; nsplit = 1 is fa2_fwd_kv_f16 and needs none.  1 <= nsplit <= 1024.
+ * aligned; nsplit = 1 is fa2_fwd_kv_f16 and needs none.  1 <= nsplit <= 1024
+ * and B*H*ceil(S/128)*nsplit < 2^31 (the grid), else FA2_ERR_BAD_SHAPE.
  * Same results as fa2_fwd_kv_f16 up to fp32 rounding of the merge.
  * No counterpart in the reference (see fa2_fwd_kv_f16). */
 size_t fa2_fwd_kv_workspace_bytes(int32_t B, int32_t H, int32_t S, int32_t nsplit);

@@ -96,6 +96,10 @@ def test_fwd_kv_split_validation():
     for nsplit, status in ((0, 4), (1025, 4), (4, 5)):   # bad counts; nsplit > 1 without a workspace
         rc = lib.fa2_fwd_kv_split_f16(ctypes.byref(p), 64, 0, nsplit, None, 0, None)
         assert rc == status, (nsplit, rc, lib.fa2_last_error())
+    # B*H*S within limits, but B*H*ceil(S/128)*nsplit past the int32 grid: rejected as a shape
+    p = _dummy_fwd(B=1 << 22, H=1, S=2)
+    rc = lib.fa2_fwd_kv_split_f16(ctypes.byref(p), 64, 0, 1024, None, 0, None)
+    assert rc == 2, (rc, lib.fa2_last_error())
 
 
 def test_empty_problem_is_a_noop():

@@ -120,6 +120,10 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     if (coff < -(1 << 30) || coff > (1 << 30))
         return fail(FA2_ERR_BAD_ARGUMENT, "causal offset %d outside +-2^30", coff);
     if (nsplit > 1) {
+        // one workgroup per (128-query block, slice, b*h); one per (slice, b*h) for decode
+        if ((double)p->B * p->H * ((p->S + 127) / 128) * nsplit > 2147483647.0)
+            return fail(FA2_ERR_BAD_SHAPE, "B*H*ceil(S/128)*nsplit = %.0f exceeds the int32 grid limit",
+                        (double)p->B * p->H * ((p->S + 127) / 128) * nsplit);
         const size_t need = kv_part_bytes(p->B, p->H, p->S, nsplit);
         if (!workspace || workspace_bytes < need)
             return fail(FA2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : 0);
