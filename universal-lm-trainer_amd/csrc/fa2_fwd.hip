@@ -483,48 +483,82 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         if (t + 1 < ntiles) general(t + 1, s1, p1, s0, p0);
     }
 
+    // Outputs leave the MFMA accumulators with each lane holding one query
+    // and runs of 4 consecutive columns, so direct stores would touch 32 rows
+    // per instruction in 8- or 16-byte pieces.  Each wave transposes its block
+    // through a private, XOR-swizzled slice of the tile stages instead (idle
+    // now: every wave is past its last tile read and no transfer is in
+    // flight), then stores whole rows with 16-byte lanes.
+    static_assert(sizeof(sKV) >= NW * QB * 8192, "output staging fits in the tile stages");
+    char *const stage_base = reinterpret_cast<char *>(&sKV[0][0][0]);
     if (SPLIT) {
         // Partial result of this slice: the O^T accumulator, the reference
         // max and the row sum (all relative to 2^msc), for the combine step.
+        // Rows of 64 fp32 (256 bytes, 16 chunks): lane (c, g2) holds logical
+        // chunks 8*db + 2*i + g2 of row c, stored at chunk ^ (c & 15).
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
+            char *blk = stage_base + 8192 * (QB * wave + qb);
             const float lt = l[qb] + xor32(l[qb]);
             const int q = qw0 + 32 * qb + c;
-            if (q < S) {
-                const int64_t row = ((int64_t)ks * BH + bh) * S + q;
-                float *po = a.part_o + row * HD;
-#pragma unroll
-                for (int db = 0; db < 2; ++db)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        f4 x;
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j];
-                        *reinterpret_cast<f4 *>(po + 32 * db + 8 * i + 4 * g2) = x;
-                    }
-                if (g2 == 0) *reinterpret_cast<f2 *>(a.part_ml + 2 * row) = f2{msc[qb], lt};
-            }
-        }
-        return;
-    }
-    // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const float lt = l[qb] + xor32(l[qb]);
-        const int q = qw0 + 32 * qb + c;
-        if (q < S) {
-            const float inv = lt > 0.f ? 1.f / lt : 0.f;
-            _Float16 *orow = Op + (int64_t)q * a.oss;
+            const int64_t row0 = ((int64_t)ks * BH + bh) * S + qw0 + 32 * qb;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     f4 x;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j] * inv;
-                    *reinterpret_cast<h4 *>(orow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(x, h4);
+                    for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j];
+                    *reinterpret_cast<f4 *>(blk + c * 256 + (((8 * db + 2 * i + g2) ^ (c & 15)) << 4)) = x;
                 }
-            if (g2 == 0) Lp[q] = (msc[qb] == -INFINITY) ? -INFINITY : (msc[qb] + log2f(lt)) * LN2;
+            if (q < S && g2 == 0) *reinterpret_cast<f2 *>(a.part_ml + 2 * (row0 + c)) = f2{msc[qb], lt};
+            const int ch = lane & 15;   // lane: chunk ch of rows 4k + (lane >> 4)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int r = 4 * k + (lane >> 4);
+                const f4 v = *reinterpret_cast<const f4 *>(blk + r * 256 + ((ch ^ (r & 15)) << 4));
+                if (qw0 + 32 * qb + r < S) *reinterpret_cast<f4 *>(a.part_o + (row0 + r) * HD + 4 * ch) = v;
+            }
+        }
+        return;
+    }
+    // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
+    // Rows of 64 fp16 (128 bytes, 8 chunks): lane (c, g2) holds half g2 of
+    // logical chunks 4*db + i of row c, stored at chunk ^ (c & 7); rows are
+    // read back as 8 lanes x 16 bytes (two 8-byte halves when O's strides are
+    // not multiples of 8 elements).
+    const bool o16 = ((a.osb | a.osh | a.oss) & 7) == 0;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        char *blk = stage_base + 4096 * (QB * wave + qb);
+        const float lt = l[qb] + xor32(l[qb]);
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f4 x;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j] * inv;
+                *reinterpret_cast<h4 *>(blk + c * 128 + (((4 * db + i) ^ (c & 7)) << 4) + 8 * g2) =
+                    __builtin_convertvector(x, h4);
+            }
+        const int q = qw0 + 32 * qb + c;
+        if (q < S && g2 == 0) Lp[q] = (msc[qb] == -INFINITY) ? -INFINITY : (msc[qb] + log2f(lt)) * LN2;
+        const int ch = lane & 7;   // lane: chunk ch of rows 8k + (lane >> 3)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int r = 8 * k + (lane >> 3);
+            const h8 v = *reinterpret_cast<const h8 *>(blk + r * 128 + ((ch ^ (r & 7)) << 4));
+            if (qw0 + 32 * qb + r < S) {
+                _Float16 *dst = Op + (int64_t)(qw0 + 32 * qb + r) * a.oss + 8 * ch;
+                if (o16) {
+                    *reinterpret_cast<h8 *>(dst) = v;
+                } else {
+                    *reinterpret_cast<h4 *>(dst) = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+                    *reinterpret_cast<h4 *>(dst + 4) = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+                }
+            }
         }
     }
 }
