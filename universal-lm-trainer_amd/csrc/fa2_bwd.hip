@@ -414,23 +414,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     // Tiles after this wave's last: keep joining the barriers and moving tiles.
     for (int t = max(tlast + 1, 0); t < ntiles - 1; ++t) tile_end(t);
 
+    // dQ rows leave through LDS (store_rows_f16).  The last tile has no
+    // barrier after it, so other waves may still read the stages of tiles
+    // ntiles-1 and ntiles-2; the other two stages are idle (their last
+    // reads precede the barrier of tile ntiles-2, and the last transfer went
+    // into the stage of tile ntiles-1): waves 0, 1 use stage ntiles % 4,
+    // waves 2, 3 stage (ntiles + 1) % 4, 4 KB per 32-query block.
+    static_assert(QP_NST == 4 && DQ_QB == 2 && sizeof(sKV[0]) == 16384, "dQ staging layout");
     const float sc = a.scale;
+    const bool dq16 = ((a.dqsb | a.dqsh | a.dqss) & 7) == 0;
+    char *const stg = reinterpret_cast<char *>(sKV[stage_of(ntiles + (wave >> 1))]) + 8192 * (wave & 1);
 #pragma unroll
-    for (int qb = 0; qb < DQ_QB; ++qb) {
-        const int q = qw0 + 32 * qb + c;
-        if (q < S) {
-            _Float16 *row = dQp + q * a.dqss;
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    f4 x;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) x[j] = dq[qb][db][4 * i + j] * sc;
-                    *reinterpret_cast<h4 *>(row + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(x, h4);
-                }
-        }
-    }
+    for (int qb = 0; qb < DQ_QB; ++qb)
+        store_rows_f16(dq[qb][0], dq[qb][1], sc, stg + 4096 * qb, dQp + (int64_t)(qw0 + 32 * qb) * a.dqss, a.dqss,
+                       S - (qw0 + 32 * qb), dq16);
 }
 
 // ---------------------------------------------------------------------------
@@ -1117,24 +1114,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         }
     }
 
+    // dK, dV rows leave through LDS (store_rows_f16): after the last tile's
+    // barrier no wave reads the stages and no transfer is in flight, so wave
+    // w uses 8 KB of them.
+    static_assert(sizeof(sQD) >= KP_NW * 8192, "dK/dV staging fits in the stages");
     const float sc = a.scale;
-    if (key < S) {
-        _Float16 *krow = dKp + (int64_t)key * a.dkss;
-        _Float16 *vrow = dVp + (int64_t)key * a.dvss;
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f4 xk, xv;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    xk[j] = dk[db][4 * i + j] * sc;
-                    xv[j] = dv[db][4 * i + j];
-                }
-                *reinterpret_cast<h4 *>(krow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xk, h4);
-                *reinterpret_cast<h4 *>(vrow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xv, h4);
-            }
-    }
+    char *const stg = reinterpret_cast<char *>(&sQD[0][0][0]) + 8192 * wave;
+    store_rows_f16(dk[0], dk[1], sc, stg, dKp + (int64_t)kw0 * a.dkss, a.dkss, S - kw0,
+                   ((a.dksb | a.dksh | a.dkss) & 7) == 0);
+    store_rows_f16(dv[0], dv[1], 1.f, stg + 4096, dVp + (int64_t)kw0 * a.dvss, a.dvss, S - kw0,
+                   ((a.dvsb | a.dvsh | a.dvss) & 7) == 0);
 }
 
 }  // namespace

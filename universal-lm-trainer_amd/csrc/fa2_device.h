@@ -319,6 +319,45 @@ __device__ __forceinline__ h8 neg_h8(h8 v) { return -v; }
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
 
+// Stores a wave's 32 x 64 output block held as two 32x32 MFMA accumulators
+// (acc0: columns 0..31, acc1: 32..63 of each row; lane (c, g2) holds row c,
+// columns 32*db + 8i + 4*g2 + j in element 4i + j), scaled by `mul`, as fp16
+// rows dst + r * stride for r < nrows.  Direct stores would touch 32 rows per
+// instruction in 8-byte pieces; the block goes through `blk`, a 4 KB
+// wave-private LDS slice no other wave touches meanwhile (row r, 16-byte
+// chunk ch at chunk ch ^ (r & 7): conflict-free both ways), and leaves as
+// whole 128-byte rows, 8 lanes x 16 bytes (8-byte halves unless `vec16`:
+// dst and stride multiples of 8 elements).
+__device__ __forceinline__ void store_rows_f16(const f16x &acc0, const f16x &acc1, float mul, char *blk,
+                                               _Float16 *dst, int64_t stride, int nrows, bool vec16) {
+    const int lane = threadIdx.x & 63, c = lane & 31, g2 = lane >> 5;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f4 x;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[j] = (db ? acc1 : acc0)[4 * i + j] * mul;
+            *reinterpret_cast<h4 *>(blk + c * 128 + (((4 * db + i) ^ (c & 7)) << 4) + 8 * g2) =
+                __builtin_convertvector(x, h4);
+        }
+    const int ch = lane & 7;   // lane: chunk ch of rows 8k + (lane >> 3)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int r = 8 * k + (lane >> 3);
+        const h8 v = *reinterpret_cast<const h8 *>(blk + r * 128 + ((ch ^ (r & 7)) << 4));
+        if (r < nrows) {
+            _Float16 *p = dst + r * stride + 8 * ch;
+            if (vec16) {
+                *reinterpret_cast<h8 *>(p) = v;
+            } else {
+                *reinterpret_cast<h4 *>(p) = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+                *reinterpret_cast<h4 *>(p + 4) = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+            }
+        }
+    }
+}
+
 // acc + sum of the eight halves, two per v_dot2_f32_f16 (fp32 accumulation).
 __device__ __forceinline__ float sum_h8(h8 v, float acc) {
     const h2 one = {(_Float16)1.0f, (_Float16)1.0f};

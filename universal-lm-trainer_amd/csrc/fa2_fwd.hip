@@ -523,43 +523,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         return;
     }
     // Epilogue: O = acc / l (l == 0 -> 0), LSE = (m*scale2 + log2 l) * ln 2.
-    // Rows of 64 fp16 (128 bytes, 8 chunks): lane (c, g2) holds half g2 of
-    // logical chunks 4*db + i of row c, stored at chunk ^ (c & 7); rows are
-    // read back as 8 lanes x 16 bytes (two 8-byte halves when O's strides are
-    // not multiples of 8 elements).
+    // O rows leave through this wave's 4 KB slice of the stages.
     const bool o16 = ((a.osb | a.osh | a.oss) & 7) == 0;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        char *blk = stage_base + 4096 * (QB * wave + qb);
         const float lt = l[qb] + xor32(l[qb]);
-        const float inv = lt > 0.f ? 1.f / lt : 0.f;
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f4 x;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) x[j] = o[qb][db][4 * i + j] * inv;
-                *reinterpret_cast<h4 *>(blk + c * 128 + (((4 * db + i) ^ (c & 7)) << 4) + 8 * g2) =
-                    __builtin_convertvector(x, h4);
-            }
         const int q = qw0 + 32 * qb + c;
         if (q < S && g2 == 0) Lp[q] = (msc[qb] == -INFINITY) ? -INFINITY : (msc[qb] + log2f(lt)) * LN2;
-        const int ch = lane & 7;   // lane: chunk ch of rows 8k + (lane >> 3)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int r = 8 * k + (lane >> 3);
-            const h8 v = *reinterpret_cast<const h8 *>(blk + r * 128 + ((ch ^ (r & 7)) << 4));
-            if (qw0 + 32 * qb + r < S) {
-                _Float16 *dst = Op + (int64_t)(qw0 + 32 * qb + r) * a.oss + 8 * ch;
-                if (o16) {
-                    *reinterpret_cast<h8 *>(dst) = v;
-                } else {
-                    *reinterpret_cast<h4 *>(dst) = __builtin_shufflevector(v, v, 0, 1, 2, 3);
-                    *reinterpret_cast<h4 *>(dst + 4) = __builtin_shufflevector(v, v, 4, 5, 6, 7);
-                }
-            }
-        }
+        store_rows_f16(o[qb][0], o[qb][1], lt > 0.f ? 1.f / lt : 0.f, stage_base + 4096 * (QB * wave + qb),
+                       Op + (int64_t)(qw0 + 32 * qb) * a.oss, a.oss, S - (qw0 + 32 * qb), o16);
     }
 }
 
