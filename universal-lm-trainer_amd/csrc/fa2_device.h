@@ -325,7 +325,8 @@ __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
 // rows dst + r * stride for r < nrows.  Direct stores would touch 32 rows per
 // instruction in 8-byte pieces; the block goes through `blk`, a 4 KB
 // wave-private LDS slice no other wave touches meanwhile (row r, 16-byte
-// chunk ch at chunk ch ^ (r & 7): conflict-free both ways), and leaves as
+// chunk ch at chunk ch ^ (r & 7): the row reads are conflict-free, the
+// 8-byte writes put rows 8 apart on the same banks), and leaves as
 // whole 128-byte rows, 8 lanes x 16 bytes (8-byte halves unless `vec16`:
 // dst and stride multiples of 8 elements).
 __device__ __forceinline__ void store_rows_f16(const f16x &acc0, const f16x &acc1, float mul, char *blk,
