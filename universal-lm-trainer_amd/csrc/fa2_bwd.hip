@@ -147,53 +147,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     const int qw0 = q_wg0 + wave * 32 * DQ_QB;
     const float scale2 = a.scale2;
 
-    // Resident Q^T / dO^T operands, delta and log2-scaled LSE of the wave's
-    // queries (rows past S: row S - 1 and LSE = +inf, so P = dS = 0).
-    h8 qf[DQ_QB][4], dof[DQ_QB][4];
-    float lse2[DQ_QB], dl[DQ_QB];
-#pragma unroll
-    for (int qb = 0; qb < DQ_QB; ++qb) {
-        const int q = qw0 + 32 * qb + c;
-        const bool valid = q < S;
-        const int qr = min(q, S - 1);
-        float part = 0.f;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const int d0 = 16 * st + 8 * g2;
-            const h8 qv = *reinterpret_cast<const h8 *>(Qp + (int64_t)qr * a.qss + d0);
-            const h8 dv = *reinterpret_cast<const h8 *>(dOp + (int64_t)qr * a.doss + d0);
-            const h8 ov = *reinterpret_cast<const h8 *>(Op + (int64_t)qr * a.oss + d0);
-            qf[qb][st] = a.negate ? neg_h8(qv) : qv;
-            dof[qb][st] = dv;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)dv[e];
-        }
-        dl[qb] = part + xor32(part);
-        lse2[qb] = valid ? Lp[qr] * LOG2E : INFINITY;
-        if (valid && g2 == 0) {   // for the dK/dV pass
-            Dp[q] = dl[qb];
-            a.lse2[(int64_t)bh * S + q] = lse2[qb];
-            store_row_terms(a, bh, q, lse2[qb], dl[qb]);
-        }
-    }
-
-    f16x dq[DQ_QB][2];
-#pragma unroll
-    for (int qb = 0; qb < DQ_QB; ++qb) {
-        dq[qb][0] = zero16();
-        dq[qb][1] = zero16();
-    }
-    // Without dropout, dP^T - delta comes out of the MFMA chain: one extra
-    // bf16 step adds ones(k) * (-delta split into three bf16 parts, exact to
-    // fp32 rounding) over k = 0..2, so dS = P * acc needs no subtraction.
-    // Lanes of k half 1 (g2 = 1) hold zeros in both operands.
-    b8 dmb[DQ_QB], ones3;
-    if (!DROPOUT) {
-#pragma unroll
-        for (int qb = 0; qb < DQ_QB; ++qb) dmb[qb] = g2 == 0 ? split3_bf16(-dl[qb]) : zero_b8();
-        ones3 = g2 == 0 ? ones3_b8() : zero_b8();
-    }
-
+    // The first key tiles go out before the wave's Q, dO and O rows are
+    // loaded: the delta computation waits for those rows, and with the
+    // transfers already in flight the two round trips overlap.
     const int kend = CAUSAL ? min(S, q_wg0 + DQ_QWG) : S;
     const int ntiles = (kend + DQ_KT - 1) / DQ_KT;
     // Last key tile of this wave (-1: none).  The wave's first query is a
@@ -246,6 +202,54 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
 #pragma unroll
     for (int t = 0; t < QP_NST - 1; ++t)
         if (t < ntiles) issue(t);
+
+    // Resident Q^T / dO^T operands, delta and log2-scaled LSE of the wave's
+    // queries (rows past S: row S - 1 and LSE = +inf, so P = dS = 0).
+    h8 qf[DQ_QB][4], dof[DQ_QB][4];
+    float lse2[DQ_QB], dl[DQ_QB];
+#pragma unroll
+    for (int qb = 0; qb < DQ_QB; ++qb) {
+        const int q = qw0 + 32 * qb + c;
+        const bool valid = q < S;
+        const int qr = min(q, S - 1);
+        float part = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int d0 = 16 * st + 8 * g2;
+            const h8 qv = *reinterpret_cast<const h8 *>(Qp + (int64_t)qr * a.qss + d0);
+            const h8 dv = *reinterpret_cast<const h8 *>(dOp + (int64_t)qr * a.doss + d0);
+            const h8 ov = *reinterpret_cast<const h8 *>(Op + (int64_t)qr * a.oss + d0);
+            qf[qb][st] = a.negate ? neg_h8(qv) : qv;
+            dof[qb][st] = dv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)dv[e];
+        }
+        dl[qb] = part + xor32(part);
+        lse2[qb] = valid ? Lp[qr] * LOG2E : INFINITY;
+        if (valid && g2 == 0) {   // for the dK/dV pass
+            Dp[q] = dl[qb];
+            a.lse2[(int64_t)bh * S + q] = lse2[qb];
+            store_row_terms(a, bh, q, lse2[qb], dl[qb]);
+        }
+    }
+
+    f16x dq[DQ_QB][2];
+#pragma unroll
+    for (int qb = 0; qb < DQ_QB; ++qb) {
+        dq[qb][0] = zero16();
+        dq[qb][1] = zero16();
+    }
+    // Without dropout, dP^T - delta comes out of the MFMA chain: one extra
+    // bf16 step adds ones(k) * (-delta split into three bf16 parts, exact to
+    // fp32 rounding) over k = 0..2, so dS = P * acc needs no subtraction.
+    // Lanes of k half 1 (g2 = 1) hold zeros in both operands.
+    b8 dmb[DQ_QB], ones3;
+    if (!DROPOUT) {
+#pragma unroll
+        for (int qb = 0; qb < DQ_QB; ++qb) dmb[qb] = g2 == 0 ? split3_bf16(-dl[qb]) : zero_b8();
+        ones3 = g2 == 0 ? ones3_b8() : zero_b8();
+    }
+
     // End of tile t's third step: tile t+1 landed (tiles up to t+2 are issued,
     // 4 transfers per tile and wave), the barrier publishes it and frees the
     // stage of tile t-1 (last read by step 4t), and tile t+3 goes into it.
