@@ -214,6 +214,49 @@ def test_capi_direct_matches_binding(fa):
     assert torch.allclose(ws[: B * H * S], delta, atol=1e-3, rtol=1e-3)
 
 
+def test_capi_outputs_with_4_element_row_strides(fa):
+    """O, dQ, dK, dV written through the C ABI into padded buffers whose row stride (68 elements) is a
+    multiple of 4 but not of 8 -- accepted by the ABI, and the output stores' 8-byte path: the same bits
+    as the binding's contiguous outputs, and the padding (NaN) untouched."""
+    say("case C ABI outputs with 68-element rows")
+    lib = capi.load()
+    q, k, v, do = rand_inputs(2, 3, 200, seed=23)
+    B, H, S, _ = q.shape
+    bufs = [torch.full((B, H, S, 68), float("nan"), dtype=torch.float16, device=DEV) for _ in range(4)]
+    o, dq, dk, dv = (t[..., :64] for t in bufs)
+    assert o.stride(2) == 68 and o.data_ptr() % 16 == 0
+    lse = torch.empty(B, H, S, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = capi.fwd_params(q, k, v, o, lse, 0.125)
+    assert lib.fa2_fwd_f16(ctypes.byref(p), stream) == 0, lib.fa2_last_error()
+    ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4, device=DEV)
+    # O is an input of the backward, whose rows the ABI wants 16-byte aligned: a contiguous copy.
+    pb = capi.bwd_params(q, k, v, o.contiguous(), lse, do, dq, dk, dv, 0.125)
+    assert lib.fa2_bwd_f16(ctypes.byref(pb), 7, ws.data_ptr(), ws.numel() * 4, stream) == 0, lib.fa2_last_error()
+    torch.cuda.synchronize()
+    ref = run_kernel(fa, q, k, v, do)
+    for name, got, want in zip(("o", "lse", "dq", "dk", "dv"), (o, lse, dq, dk, dv), ref):
+        assert torch.equal(got, want), name
+    for name, t in zip(("o", "dq", "dk", "dv"), bufs):
+        assert torch.isnan(t[..., 64:]).all(), f"{name}: padding written"
+
+
+def test_empty_inputs(fa):
+    """Empty batch / sequence: outputs of the right (empty) shapes, no launch, no error."""
+    say("case empty inputs")
+    ext = fa.extension()
+    for shape in ((0, 2, 16, 64), (2, 3, 0, 64)):
+        q, k, v, do = (torch.empty(shape, dtype=torch.float16, device=DEV) for _ in range(4))
+        o, lse = ext.fa_fwd(q, k, v, 0.0, True, 0.125, 0)
+        assert o.shape == q.shape and lse.shape == q.shape[:3]
+        dq, dk, dv = ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, 0.125, 0, 7)
+        assert dq.shape == dk.shape == dv.shape == q.shape
+        kk = torch.empty(shape[0], shape[1], 5, 64, dtype=torch.float16, device=DEV)
+        o2, lse2 = ext.fa_fwd_kv(q, kk, kk, True, 0.125, 0)
+        assert o2.shape == q.shape and lse2.shape == q.shape[:3]
+    torch.cuda.synchronize()
+
+
 def test_capi_split_modes(fa):
     """dQ (mode 2) then dK/dV (mode 4) as two calls sharing one workspace give the bits of mode 7;
     delta-only (mode 1) then mode 4 matches the oracle (its delta sums in another order)."""

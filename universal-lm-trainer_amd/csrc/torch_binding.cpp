@@ -37,6 +37,12 @@ void check_status(int rc, const char *op) {
     TORCH_CHECK(rc == FA2_OK, op, ": ", fa2_status_string(rc), ": ", fa2_last_error());
 }
 
+// The C ABI takes B, H, S as int32.
+void check_dims(const torch::Tensor &t, const char *op) {
+    TORCH_CHECK(t.size(0) <= INT32_MAX && t.size(1) <= INT32_MAX && t.size(2) <= INT32_MAX, op,
+                ": B, H and S must fit in int32");
+}
+
 void strides3(const torch::Tensor &t, int64_t out[3]) {
     out[0] = t.stride(0);
     out[1] = t.stride(1);
@@ -59,6 +65,7 @@ void check_qkv(const torch::Tensor &q, const torch::Tensor &k, const torch::Tens
 std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor &k, const torch::Tensor &v,
                                     double dropout_p, bool causal, double softmax_scale, int64_t seed,
                                     int64_t causal_offset, const char *op, int64_t nsplit = 1) {
+    check_dims(q, op);
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     const int64_t B = q.size(0), H = q.size(1), S = q.size(2);
     // O follows q's memory order the way an eager elementwise output would:
@@ -140,6 +147,7 @@ std::vector<torch::Tensor> fa_fwd_kv(torch::Tensor q, torch::Tensor k, torch::Te
     TORCH_CHECK(k.device() == q.device() && v.device() == q.device(), "q/k/v device mismatch");
     TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1, "last dim must be contiguous");
     TORCH_CHECK(nsplit >= 0 && nsplit <= 1024, "nsplit must be 0 (automatic) .. 1024");
+    if (nsplit == 0 && q.numel() == 0) nsplit = 1;   // nothing to run (and no grid to size)
     if (nsplit == 0)
         nsplit = q.size(2) == 1 ? auto_nsplit_decode(q.size(0) * q.size(1), k.size(2))
                                 : auto_nsplit((q.size(2) + 127) / 128 * q.size(0) * q.size(1), (k.size(2) + 63) / 64);
@@ -156,6 +164,7 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
                     lse.size(1) == q.size(1) && lse.size(2) == q.size(2),
                 "lse must be fp32 (B,H,S)");
     TORCH_CHECK(mode >= 0 && mode <= 15, "mode must be a bit mask in 0..15");
+    check_dims(q, "fa_bwd");
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     // The kernels take any (b,h,s) strides; only rows must be contiguous and
     // 16-byte aligned.  lse must have unit stride along s.
@@ -246,6 +255,7 @@ void rope_check(const torch::Tensor &q, const torch::Tensor &k, const torch::Ten
 std::vector<torch::Tensor> rope_run(const torch::Tensor &x, const torch::Tensor &y, const torch::Tensor &cos,
                                     const torch::Tensor &sin, const torch::Tensor &shape_q,
                                     const torch::Tensor &shape_k, bool backward) {
+    check_dims(x, backward ? "rope_bwd" : "rope_fwd");
     at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
     auto qo = torch::empty_strided(shape_q.sizes(), rope_out_strides(shape_q), shape_q.options());
     auto ko = torch::empty_strided(shape_k.sizes(), rope_out_strides(shape_k), shape_k.options());
