@@ -57,9 +57,28 @@ typedef struct fa2_fwd_params {
     float dropout_p;                /* 0 <= p < 1                              */
     uint32_t seed;                  /* dropout hash seed                       */
     int32_t causal;                 /* nonzero: key j visible to query i iff j <= i */
+    uint32_t *dropout_mask;         /* optional keep-bit output, see below; NULL = none */
 } fa2_fwd_params;
 
 int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
+
+/* Dropout keep bits.  With dropout_p > 0 and dropout_mask non-NULL,
+ * fa2_fwd_f16 also stores the keep bit of every (query, key) pair it computes
+ * -- the same bits its dropout hash draws -- into dropout_mask
+ * (fa2_dropout_mask_bytes(B, H, S) bytes, 16-byte aligned; words it does not
+ * compute, such as those above the causal diagonal, are left as they were).
+ * fa2_bwd_f16 given the same words in its dropout_mask (with the same B, H,
+ * S, causal, dropout_p and seed) reads them instead of hashing again: the
+ * results are identical, the backward's hash work is gone, and the words cost
+ * one bit per pair of HBM (written once, read by the dQ and dK/dV passes).
+ * The fa2_fwd_kv_* entry points take no mask (dropout_mask must be NULL).
+ * No counterpart in the reference, which draws its dropout with curand in
+ * the forward only (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:40-364).
+ * Word layout, per (b, h), 64-key tile t (< 2*ceil(S/128)), half g (0, 1) and
+ * query i (< R = S rounded up to 256): word ((b*H + h)*T + t)*2*R + g*R + i,
+ * T = 2*ceil(S/128); its bit 16*kb + 8*hh + e is key
+ * 64*t + 32*kb + 16*hh + 8*(e/4) + 4*g + e%4 (kb, hh in 0..1, e in 0..7). */
+size_t fa2_dropout_mask_bytes(int32_t B, int32_t H, int32_t S);
 
 /* Forward over a key/value sequence of its own length, for inference callers:
  * a prefill chunk of S new queries against a KV cache of s_k rows, or decode
@@ -118,6 +137,11 @@ typedef struct fa2_bwd_params {
     float dropout_p;
     uint32_t seed;
     int32_t causal;
+    const uint32_t *dropout_mask;       /* optional: fa2_fwd_f16's keep bits (see
+                                           fa2_dropout_mask_bytes); read by the
+                                           split backward (modes 2, 4, 7), while
+                                           the fused backward hashes again, with
+                                           the same result; NULL = hash           */
 } fa2_bwd_params;
 
 /* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta and scaled LSE

@@ -1,0 +1,115 @@
+"""Dropout keep-bit words: the forward stores the keep bit of every pair it
+computes, the split backward reads them instead of hashing again.
+
+The words must hold exactly the bits of the dropout hash, so the mask path is
+checked bit for bit against the hash path (O, LSE, dQ, dK, dV identical), and
+the words themselves against the oracle's keep mask decoded through the
+layout include/fa2_mi355x.h documents.  The hash path is pinned against the
+oracle by test_gpu_parity.py::test_dropout_vs_oracle."""
+import ctypes
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import fa2_capi as capi
+from oracle import fa2_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def rand_inputs(B, H, S, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(B, H, S, 64, generator=g).half().to(DEV) for _ in range(4)]
+
+
+def mask_bits(words, B, H, S):
+    """[B*H, S, S] keep bits (query row, key col) read out of the words: word
+    ((bh*T + t)*2 + g)*R + i, bit 16*kb + 8*hh + e holds key
+    64*t + 32*kb + 16*hh + 8*(e//4) + 4*g + e%4 (T = 2*ceil(S/128), R = S rounded up to 256)."""
+    T, R = 2 * ((S + 127) // 128), (S + 255) // 256 * 256
+    w = words.reshape(B * H, T, 2, R)[:, :, :, :S]
+    j = np.arange(S)
+    t, r = j // 64, j % 64
+    kb, hh, e_hi, g, e_lo = r // 32, (r // 16) % 2, (r // 8) % 2, (r // 4) % 2, r % 4
+    bit = 16 * kb + 8 * hh + 4 * e_hi + e_lo
+    sel = w[:, t, g, :]                                  # [BH, S keys, S rows]
+    return ((sel >> bit[None, :, None].astype(np.uint32)) & 1).transpose(0, 2, 1).astype(bool)
+
+
+SHAPES = [(1, 2, 1), (1, 2, 63), (2, 2, 160), (1, 3, 257), (1, 1, 513), (2, 2, 1000)]
+
+
+@pytest.mark.parametrize("B,H,S", SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("p", [0.1, 0.5])
+def test_mask_path_bitwise_equals_hash_path(fa, B, H, S, causal, p):
+    say(f"case mask vs hash B={B} H={H} S={S} causal={causal} p={p}")
+    ext = fa.extension()
+    q, k, v, do = rand_inputs(B, H, S, seed=S + 7)
+    seed = 0x5EED + S
+    o, lse = ext.fa_fwd(q, k, v, p, causal, 0.125, seed)
+    o2, lse2, mask = ext.fa_fwd_mask(q, k, v, p, causal, 0.125, seed)
+    assert mask.dtype == torch.int32 and mask.numel() * 4 == capi.load().fa2_dropout_mask_bytes(B, H, S)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    ref = ext.fa_bwd(q, k, v, o, lse, do, p, causal, 0.125, seed, 7)
+    got = ext.fa_bwd(q, k, v, o, lse, do, p, causal, 0.125, seed, 7, mask=mask)
+    for name, a, b in zip(("dQ", "dK", "dV"), got, ref):
+        assert torch.equal(a, b), f"{name} differs"
+    # the dQ pass alone, and the dK/dV pass alone: the binding runs mode 4 as
+    # delta kernel + dK/dV, whose delta sums in another order than the dQ
+    # pass's, so it is compared with mode 4 without the words
+    dq = ext.fa_bwd(q, k, v, o, lse, do, p, causal, 0.125, seed, 2, mask=mask)[0]
+    dk, dv = ext.fa_bwd(q, k, v, o, lse, do, p, causal, 0.125, seed, 4, mask=mask)[1:]
+    dk4, dv4 = ext.fa_bwd(q, k, v, o, lse, do, p, causal, 0.125, seed, 4)[1:]
+    torch.cuda.synchronize()
+    assert torch.equal(dq, ref[0]) and torch.equal(dk, dk4) and torch.equal(dv, dv4)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("S", [70, 300])
+def test_mask_words_match_oracle_keep(fa, causal, S):
+    """Through the C ABI into a buffer prefilled with a pattern: every visible
+    pair's bit equals the oracle's keep bit (a word the forward skipped would
+    keep the pattern and fail)."""
+    say(f"case mask words S={S} causal={causal}")
+    B, H, p, seed = 2, 2, 0.3, 0xBEEF
+    q, k, v, _ = rand_inputs(B, H, S, seed=5)
+    lib = capi.load()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=DEV)
+    words = torch.full((lib.fa2_dropout_mask_bytes(B, H, S) // 4,), 0x55555555, dtype=torch.int32, device=DEV)
+    prm = capi.fwd_params(q, k, v, o, lse, 0.125, causal=causal, dropout_p=p, seed=seed, mask=words)
+    assert lib.fa2_fwd_f16(ctypes.byref(prm), None) == 0, lib.fa2_last_error()
+    torch.cuda.synchronize()
+    got = mask_bits(words.cpu().numpy().view(np.uint32), B, H, S)
+    want = orc.keep_mask(seed, B, H, S, p).reshape(B * H, S, S)
+    vis = np.ones((S, S), bool) if not causal else np.tri(S, dtype=bool)
+    bad = (got != want) & vis[None]
+    assert not bad.any(), f"{int(bad.sum())} keep bits differ, first at {np.argwhere(bad)[0]}"
+
+
+def test_autograd_mask_on_off_identical(fa, monkeypatch):
+    """flash_attn_v100 with dropout: the gradients with the keep-bit words
+    (default) equal those of the hash-only backward (mask size cap 0)."""
+    say("case autograd mask on/off")
+    q0, k0, v0, do = rand_inputs(2, 3, 384, seed=11)
+    grads = []
+    for cap in (1 << 30, 0):
+        monkeypatch.setattr(fa, "DROPOUT_MASK_MAX_BYTES", cap)
+        torch.manual_seed(1234)
+        monkeypatch.setattr(fa, "_SEED_COUNTER", itertools.count(1))
+        q, k, v = (t.clone().requires_grad_(True) for t in (q0, k0, v0))
+        o = fa.flash_attn_v100(q, k, v, dropout_p=0.2, causal=True)
+        o.backward(do)
+        grads.append([o.detach()] + [t.grad for t in (q, k, v)])
+    torch.cuda.synchronize()
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)

@@ -114,6 +114,34 @@ def test_empty_problem_is_a_noop():
     assert lib.fa2_bwd_workspace_bytes(0, 3, 5) == 0
 
 
+def test_dropout_mask_size_and_validation():
+    """Keep-bit words: per (b, h), 2*ceil(S/128) 64-key tiles x 2 halves x S rounded up to 256
+    rows, 4 bytes each; a misaligned mask is rejected only when dropout would use it, and the
+    fa2_fwd_kv_* entry points take none."""
+    lib = capi.load()
+    assert lib.fa2_dropout_mask_bytes(1, 1, 1) == 2 * 2 * 256 * 4
+    assert lib.fa2_dropout_mask_bytes(8, 12, 4096) == 96 * 64 * 2 * 4096 * 4
+    assert lib.fa2_dropout_mask_bytes(2, 3, 257) == 6 * 6 * 2 * 512 * 4
+    assert lib.fa2_dropout_mask_bytes(0, 3, 5) == 0 and lib.fa2_dropout_mask_bytes(1, 1, -1) == 0
+    p = _dummy_fwd(dropout_p=0.1, dropout_mask=(1 << 21) + 4)
+    assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 3, lib.fa2_last_error()
+    assert b"dropout_mask" in lib.fa2_last_error()
+    p = _dummy_fwd(dropout_mask=1 << 21)
+    assert lib.fa2_fwd_kv_f16(ctypes.byref(p), 16, 0, None) == 4
+    assert lib.fa2_fwd_kv_split_f16(ctypes.byref(p), 16, 0, 2, None, 0, None) == 4
+    pb = capi.BwdParams()
+    base = 1 << 20
+    pb.q = pb.k = pb.v = pb.o = pb.dout = pb.lse = pb.dq = pb.dk = pb.dv = base
+    for f in ("q_stride", "k_stride", "v_stride", "o_stride", "do_stride", "dq_stride", "dk_stride", "dv_stride"):
+        setattr(pb, f, capi.I64x3(64 * 64, 64 * 64, 64))
+    pb.lse_stride = capi.I64x2(64, 64)
+    pb.B, pb.H, pb.S, pb.D, pb.softmax_scale, pb.dropout_p = 1, 1, 64, 64, 0.125, 0.1
+    pb.dropout_mask = base + 8
+    need = lib.fa2_bwd_workspace_bytes(1, 1, 64)
+    assert lib.fa2_bwd_f16(ctypes.byref(pb), 7, ctypes.c_void_p(1 << 22), need, None) == 3
+    assert b"dropout_mask" in lib.fa2_last_error()
+
+
 def test_bwd_validation():
     lib = capi.load()
     p = capi.BwdParams()

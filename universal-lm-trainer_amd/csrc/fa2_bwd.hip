@@ -119,9 +119,16 @@ constexpr int QP_NST = 4;   // LDS stages: key tiles t-1, t, t+1 resident, t+2 i
 // A unit reads its K / V fragments from LDS itself rather than sharing them
 // between the two query blocks, which keeps two units in flight within 256
 // registers.
-template <bool CAUSAL, bool DROPOUT>
+//
+// DMASK (dropout with a.drop_mask): the keep bits come from the words the
+// forward wrote (two per query and key tile, moved into LDS with the tile)
+// instead of the hash.
+template <bool CAUSAL, bool DROPOUT, bool DMASK>
 __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
+    static_assert(!DMASK || DROPOUT, "keep-bit words only with dropout");
     __shared__ __attribute__((aligned(16))) h8 sKV[QP_NST][2][DQ_KT * 8];
+    // DMASK: per stage and wave, the words of its 64 queries for halves g2 = 0, 1.
+    __shared__ __attribute__((aligned(16))) uint32_t sMQ[DMASK ? QP_NST : 1][DQ_NW][2][64];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -185,6 +192,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     int kn = 0;          // first key of the next tile to issue
     uint32_t stn = 0;    // its stage
     const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 2048u * (uint32_t)wave;
+    // DMASK: the wave's 64 words per half g2 of each tile (rows past S are
+    // within the mask's padded rows), 4 bytes per lane.
+    const uint32_t lds_mq = lds_addr(&sMQ[0][wave][0][0]);
     auto issue = [&](int) FA2_INLINE {
         uint32_t ko[2], vo[2];
         tile_offsets(kn, ko, vo);
@@ -193,6 +203,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
             const uint32_t d = lds_kv + stn * (uint32_t)sizeof(sKV[0]) + 1024u * (uint32_t)i;
             lds_dma16_at(gk, ko[i], d);
             lds_dma16_at(gv, vo[i], d + (uint32_t)sizeof(sKV[0][0]));
+        }
+        if (DMASK) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+                lds_dma4_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(bh, S, kn / DQ_KT, half, qw0)),
+                            4u * (uint32_t)lane, lds_mq + stn * (uint32_t)sizeof(sMQ[0]) + 256u * (uint32_t)half);
         }
         gk += k_step;
         gv += v_step;
@@ -251,10 +267,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     }
 
     // End of tile t's third step: tile t+1 landed (tiles up to t+2 are issued,
-    // 4 transfers per tile and wave), the barrier publishes it and frees the
-    // stage of tile t-1 (last read by step 4t), and tile t+3 goes into it.
+    // 4 transfers per tile and wave, 6 with DMASK), the barrier publishes it
+    // and frees the stage of tile t-1 (last read by step 4t), and tile t+3
+    // goes into it.
     auto tile_end = [&](int t) FA2_INLINE {
-        if (t + 2 < ntiles) vm_wait<4>(); else vm_wait<0>();
+        if (t + 2 < ntiles) vm_wait<DMASK ? 6 : 4>(); else vm_wait<0>();
         lds_barrier();
         if (t + QP_NST - 1 < ntiles) issue(t + QP_NST - 1);
     };
@@ -309,17 +326,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     };
     // dS of element r of unit (t, kb, qb) from its score and dP value.
     // (Without dropout g is dP - delta already.)
-    auto ds_of = [&](float sv, float g, int t, int kb, int qb, int r) FA2_INLINE {
+    // DMASK: mw is the unit's keep word (query qw0 + 32*qb + c, tile t, half
+    // g2), whose bit 16*kb + r is element r's.
+    auto ds_of = [&](float sv, float g, int t, int kb, int qb, int r, uint32_t mw) FA2_INLINE {
         const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -lse2[qb]));
         if (!DROPOUT) return p * g;
         const int key = t * DQ_KT + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-        g = dropout_keep(a.seed, qw0 + 32 * qb + c, key, (uint32_t)bh, a.drop_thr) ? g * a.inv_keep : 0.f;
+        const bool keep = DMASK ? ((mw >> (16 * kb + r)) & 1u) != 0
+                                : dropout_keep(a.seed, qw0 + 32 * qb + c, key, (uint32_t)bh, a.drop_thr);
+        g = keep ? g * a.inv_keep : 0.f;
         return p * (g - dl[qb]);
+    };
+    auto keep_word = [&](int t, int qb) FA2_INLINE -> uint32_t {
+        return DMASK ? sMQ[DMASK ? stage_of(t) : 0][wave][g2][32 * qb + c] : 0u;
     };
     auto ds_form = [&](int t, int kb, int qb, const f16x &s, const f16x &dp, h8(&dsb)[2]) FA2_INLINE {
         f16x x;
+        const uint32_t mw = keep_word(t, qb);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] = ds_of(s[r], dp[r], t, kb, qb, r);
+        for (int r = 0; r < 16; ++r) x[r] = ds_of(s[r], dp[r], t, kb, qb, r, mw);
         dsb[0] = acc_to_h8(x, 0);
         dsb[1] = acc_to_h8(x, 1);
     };
@@ -333,6 +358,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
                     int qbp, const h8(&ds_p)[2], int sn, int kbn, int qbn, f16x &s_n, f16x &dp_n) FA2_INLINE {
         h8 n0 = trk(sp, kbp, 0, 0), n1 = trk(sp, kbp, 1, 0);
         float x[16];
+        const uint32_t mw = keep_word(t, qb);
 #pragma unroll
         for (int i = 0; i < 6; ++i) {
             const h8 f0 = n0, f1 = n1;
@@ -358,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
             const int ehi = i < 3 ? 3 * i + 3 : 12 + 2 * (i - 3);
 #pragma unroll
             for (int e = elo; e < ehi; ++e) {
-                x[e] = ds_of(s_c[e], dp_c[e], t, kb, qb, e);
+                x[e] = ds_of(s_c[e], dp_c[e], t, kb, qb, e, mw);
                 if (e & 1) {
                     const f2 xx = {x[e - 1], x[e]};
                     const h2 hd = __builtin_convertvector(xx, h2);
@@ -376,7 +402,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     f16x sA, dpA, sB, dpB;
     h8 dsA[2], dsB[2];
     // Tile 0 landed once at most the transfers of tiles 1 and 2 are pending.
-    if (ntiles >= 3) vm_wait<8>(); else if (ntiles == 2) vm_wait<4>(); else vm_wait<0>();
+    if (ntiles >= 3) vm_wait<DMASK ? 12 : 8>(); else if (ntiles == 2) vm_wait<DMASK ? 6 : 4>(); else vm_wait<0>();
     lds_barrier();
     if (tlast >= 0) {
         sdp(0, 0, 0, sA, dpA);
@@ -750,14 +776,23 @@ static_assert(KP_NST >= 4 && KP_NST <= 6, "dK/dV stages");
 // against ones), so P = exp2(S*scale2) and dS = P * dP take no per-element
 // row statistics from LDS and no subtraction.  Otherwise the tile's lse2 and
 // delta are read from LDS per element.
-template <bool CAUSAL, bool DROPOUT, bool FOLD>
+//
+// DMASK (dropout with a.drop_mask): the keep bits come from the words the
+// forward wrote: per 32-query tile, the words of both 64-key tiles of the
+// workgroup's keys (4 runs of 32 words), moved into LDS by wave 1; each lane
+// tests one bit position of the words of its 16 query rows.
+template <bool CAUSAL, bool DROPOUT, bool FOLD, bool DMASK>
 __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     static_assert(!(FOLD && DROPOUT), "the folded row terms assume no dropout");
+    static_assert(!DMASK || DROPOUT, "keep-bit words only with dropout");
     __shared__ __attribute__((aligned(16))) h8 sQD[KP_NST][2][KP_QT * 8];   // Q, dO tiles (4 KB each)
     // Per stage: lse2[32], delta[32] (fp32); FOLD: the 512-byte block of bf16
     // row terms (and a duplicate from the transfer's upper 32 lanes).
     __shared__ __attribute__((aligned(16))) float sLD[KP_NST][FOLD ? 256 : 2 * KP_QT];
     __shared__ __attribute__((aligned(16))) uint32_t sZero[2];
+    // DMASK: per stage, run s = 2*i + g2' holds the 32 words of 64-key tile
+    // 2*kblk + i, half g2' (and a copy from the transfer's upper 32 lanes).
+    __shared__ __attribute__((aligned(16))) uint32_t sDM[DMASK ? KP_NST : 1][256];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -834,6 +869,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     int qn = q_start;          // first query of the next tile to issue
     uint32_t stn = 0;          // its stage
     const uint32_t lds_qd = lds_addr(&sQD[0][0][0]) + 1024u * (uint32_t)wave, lds_ld = lds_addr(&sLD[0][0]);
+    // DMASK: lane L of wave 1's transfer moves words 4*(L & 7) .. +3 of run
+    // s = (L & 31) >> 3, i.e. of 64-key tile 2*kblk + (s >> 1), half s & 1,
+    // at word s * dmask_rows(S) past the tile's first run (lanes 32..63
+    // repeat lanes 0..31).
+    const uint32_t dmoff = 4u * (uint32_t)(((lane & 31) >> 3) * dmask_rows(S) + 4 * (lane & 7));
+    const uint32_t lds_dm = lds_addr(&sDM[0][0]);
     auto issue = [&](int) FA2_INLINE {
         uint32_t qo = qoff0, doo = dooff0;
         if (qn + KP_QT > S) tile_offsets(qn, qo, doo);
@@ -845,6 +886,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
             else
                 lds_dma4_at(gld, ldoff_t, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
         }
+        if (DMASK && wave == 1)
+            lds_dma16_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(bh, S, 2 * kblk, 0, qn)), dmoff,
+                         lds_dm + stn * (uint32_t)sizeof(sDM[0]));
         gq += dq_step;
         gdo += ddo_step;
         gld += FOLD ? 512 : KP_QT * sizeof(float);
@@ -854,13 +898,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
 #pragma unroll
     for (int t = 0; t < KP_NST - 1; ++t)
         if (t < ntiles) issue(t);
-    // Transfers per tile and wave: 2, plus 1 for wave 0.  Wait until at most
-    // n tiles' transfers are pending.
+    // Transfers per tile and wave: 2, plus 1 for wave 0 (and, DMASK, for
+    // wave 1).  Wait until at most n tiles' transfers are pending.
+    const bool three = wave == 0 || (DMASK && wave == 1);
     auto wait_tiles = [&](int n) FA2_INLINE {
         if (n <= 0) vm_wait<0>();
-        else if (n == 1) { if (wave == 0) vm_wait<3>(); else vm_wait<2>(); }
-        else if (n == 2) { if (wave == 0) vm_wait<6>(); else vm_wait<4>(); }
-        else { if (wave == 0) vm_wait<9>(); else vm_wait<6>(); }
+        else if (n == 1) { if (three) vm_wait<3>(); else vm_wait<2>(); }
+        else if (n == 2) { if (three) vm_wait<6>(); else vm_wait<4>(); }
+        else { if (three) vm_wait<9>(); else vm_wait<6>(); }
     };
     auto tile_end = [&](int t) FA2_INLINE {
         // tile t+2 landed (tiles up to t+NST-2 issued); stage of tile t-1 free
@@ -940,7 +985,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     // value g, lse2 l and delta dl.  Dropout: dV takes the kept, rescaled P;
     // dS = P * (dP * keep / (1-p) - delta).
     // FOLD: s and g already hold S - lse2/scale2 and dP - delta.
-    auto pds = [&](float sv, float g, float l, float dl, int q, float &pd, float &ds) FA2_INLINE {
+    // DMASK: mw is the keep word of the element's query row, whose bit kbit
+    // is this lane's key (run dm_run of the tile's words).
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const int kbit = 16 * (wave & 1) + 8 * ((c >> 4) & 1) + 4 * ((c >> 3) & 1) + (c & 3);
+    const int dm_run = 2 * (wave >> 1) + ((c >> 2) & 1);
+    auto pds = [&](float sv, float g, float l, float dl, int q, uint32_t mw, float &pd, float &ds) FA2_INLINE {
         if (FOLD) {
             pd = __builtin_amdgcn_exp2f(sv * scale2);
             ds = pd * g;
@@ -948,7 +998,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         }
         const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -l));
         if (DROPOUT) {
-            const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
+            const bool keep = DMASK ? ((mw >> kbit) & 1u) != 0 : dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
             pd = keep ? p * a.inv_keep : 0.f;
             ds = pd * g - p * dl;
         } else {
@@ -957,9 +1007,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         }
     };
     // The tile's lse2 / delta for this lane's rows 8i + 4*g2 + j.
-    auto stats = [&](int stage, f4(&l4)[4], f4(&d4)[4]) FA2_INLINE {
+    // (and, DMASK, their keep words)
+    auto stats = [&](int stage, f4(&l4)[4], f4(&d4)[4], u4v(&m4)[4]) FA2_INLINE {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            m4[i] = u4v{0u, 0u, 0u, 0u};
             if (FOLD) {   // unused
                 l4[i] = f4{0.f, 0.f, 0.f, 0.f};
                 d4[i] = l4[i];
@@ -967,6 +1019,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
             }
             l4[i] = *reinterpret_cast<const f4 *>(&sLD[stage][8 * i + 4 * g2]);
             d4[i] = *reinterpret_cast<const f4 *>(&sLD[stage][KP_QT + 8 * i + 4 * g2]);
+            if (DMASK) m4[i] = *reinterpret_cast<const u4v *>(&sDM[DMASK ? stage : 0][32 * dm_run + 8 * i + 4 * g2]);
         }
     };
     // General P / dS (first and last tiles): rows past S and, causal, keys
@@ -975,7 +1028,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     auto pds_general = [&](int t, const f16x &s, const f16x &dp, h8(&pb)[2], h8(&dsb)[2]) FA2_INLINE {
         const int q0 = q_start + t * KP_QT;
         f4 l4[4], d4[4];
-        stats(stage_of(t), l4, d4);
+        u4v m4[4];
+        stats(stage_of(t), l4, d4, m4);
         const int lo = key - q0 - 4 * g2;        // visible iff off >= lo (causal)
         const int hi = S - q0 - 4 * g2;          // and off < hi
 #pragma unroll
@@ -986,7 +1040,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                 const int r = 8 * hh + e;
                 const int off = 8 * (r >> 2) + (r & 3);
                 float pd, ds;
-                pds(s[r], dp[r], l4[r >> 2][r & 3], d4[r >> 2][r & 3], q0 + 4 * g2 + off, pd, ds);
+                pds(s[r], dp[r], l4[r >> 2][r & 3], d4[r >> 2][r & 3], q0 + 4 * g2 + off, m4[r >> 2][r & 3], pd, ds);
                 const bool vis = (!CAUSAL || off >= lo) && off < hi;
                 xp[e] = vis ? pd : 0.f;
                 xd[e] = vis ? ds : 0.f;
@@ -1004,7 +1058,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                        h8(&ds_c)[2]) FA2_INLINE {
         const int q0 = q_start + t * KP_QT;
         f4 l4[4], d4[4];
-        stats(sc_, l4, d4);
+        u4v m4[4];
+        stats(sc_, l4, d4, m4);
         b8 al, ad;
         if (FOLD) {
             al = aread(sn, 0);
@@ -1047,7 +1102,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                 const int r = 2 * i + e;
                 float pd, ds;
                 pds(s_c[r], dp_c[r], l4[r >> 2][r & 3], d4[r >> 2][r & 3], q0 + 4 * g2 + 8 * (r >> 2) + (r & 3),
-                    pd, ds);
+                    m4[r >> 2][r & 3], pd, ds);
                 xp[e] = pd;
                 xd[e] = ds;
             }
@@ -1141,16 +1196,21 @@ hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st) {
 hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const int nqblk = (a.S + DQ_QWG - 1) / DQ_QWG;
     const dim3 grid((unsigned)(nqblk * a.B * a.H)), block(256);
+    const bool dmask = dropout && a.drop_mask != nullptr;
     if (causal) {
-        if (dropout)
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true>), grid, block, 0, st, a);
+        if (dmask)
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true, true>), grid, block, 0, st, a);
+        else if (dropout)
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true, false>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, false, false>), grid, block, 0, st, a);
     } else {
-        if (dropout)
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true>), grid, block, 0, st, a);
+        if (dmask)
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true, true>), grid, block, 0, st, a);
+        else if (dropout)
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true, false>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, false, false>), grid, block, 0, st, a);
     }
     return hipGetLastError();
 }
@@ -1177,20 +1237,25 @@ hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream
     const dim3 grid((unsigned)(nkblk * a.B * a.H)), block(256);
     // The folded row terms need -lse2/scale2 finite (|lse2| < 3e18 at this bound).
     const bool fold = !dropout && a.scale2 >= 1e-20f;
+    const bool dmask = dropout && a.drop_mask != nullptr;
     if (causal) {
-        if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, true, false>), grid, block, 0, st, a);
+        if (dmask)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, true, false, true>), grid, block, 0, st, a);
+        else if (dropout)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, true, false, false>), grid, block, 0, st, a);
         else if (fold)
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false, true, false>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<true, false, false, false>), grid, block, 0, st, a);
     } else {
-        if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, true, false>), grid, block, 0, st, a);
+        if (dmask)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, true, false, true>), grid, block, 0, st, a);
+        else if (dropout)
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, true, false, false>), grid, block, 0, st, a);
         else if (fold)
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false, true, false>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false, false, false>), grid, block, 0, st, a);
     }
     return hipGetLastError();
 }

@@ -68,6 +68,14 @@ float scale2_of(float scale) {
     return s2 < FLT_MIN ? FLT_MIN : s2;
 }
 
+// The keep-bit words are moved in 16-byte transfers; without dropout they
+// are not touched.
+int check_mask(const void *mask, float p) {
+    if (mask && p > 0.f && (reinterpret_cast<uintptr_t>(mask) & 15u))
+        return fail(FA2_ERR_MISALIGNED, "dropout_mask is not 16-byte aligned");
+    return FA2_OK;
+}
+
 // keep iff (hash >> 8) * 2^-24 >= p  <=>  (hash >> 8) >= ceil(p * 2^24)
 uint32_t drop_threshold(float p) { return (uint32_t)ceilf(p * 16777216.0f); }
 
@@ -96,6 +104,12 @@ static size_t kv_part_bytes(int32_t B, int32_t H, int32_t S, int32_t nsplit) {
     return (size_t)nsplit * B * H * S * (FA2_HEAD_DIM + 2) * sizeof(float);
 }
 
+size_t fa2_dropout_mask_bytes(int32_t B, int32_t H, int32_t S) {
+    if (B <= 0 || H <= 0 || S <= 0) return 0;
+    const size_t tiles = 2 * (((size_t)S + 127) / 128), rows = ((size_t)S + 255) & ~(size_t)255;
+    return (size_t)B * H * tiles * 2 * rows * sizeof(uint32_t);
+}
+
 size_t fa2_fwd_kv_workspace_bytes(int32_t B, int32_t H, int32_t S, int32_t nsplit) {
     if (B <= 0 || H <= 0 || S <= 0 || nsplit <= 1) return 0;
     return kv_part_bytes(B, H, S, nsplit);
@@ -114,6 +128,8 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     int rc = check_shape(p->B, p->H, p->S, p->D, 256);
     if (rc) return rc;
     if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
+    if (inference && p->dropout_mask)
+        return fail(FA2_ERR_BAD_ARGUMENT, "dropout_mask must be NULL for the fa2_fwd_kv_* entry points");
     if ((int64_t)p->B * p->H * p->S == 0) return FA2_OK;
     if (s_k < 1 || (double)p->B * p->H * s_k > 2147483647.0)
         return fail(FA2_ERR_BAD_SHAPE, "key length %d outside 1 .. 2^31 / (B*H)", s_k);
@@ -139,6 +155,7 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
     if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
     if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
+    if ((rc = check_mask(p->dropout_mask, p->dropout_p))) return rc;
 
     fa2::FwdArgs a;
     a.q = static_cast<const _Float16 *>(p->q);
@@ -165,6 +182,7 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     a.drop_thr = drop_threshold(p->dropout_p);
     a.inv_keep = 1.f / (1.f - p->dropout_p);
     const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
+    a.drop_mask = dropout ? p->dropout_mask : nullptr;
     const hipStream_t st = (hipStream_t)stream;
     const hipError_t e = (inference && p->S == 1 && !dropout) ? fa2::launch_fwd_decode(a, causal, st)
                          : nsplit > 1                         ? fa2::launch_fwd_split(a, causal, dropout, st)
@@ -232,6 +250,7 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
         if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
         if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
         if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
+        if ((rc = check_mask(p->dropout_mask, p->dropout_p))) return rc;
     }
     struct Out { const char *name; void *ptr; const int64_t *st; };
     const Out outs[3] = {{"dq", p->dq, p->dq_stride}, {"dk", p->dk, p->dk_stride}, {"dv", p->dv, p->dv_stride}};
@@ -277,6 +296,7 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     a.drop_thr = drop_threshold(p->dropout_p);
     a.inv_keep = 1.f / (1.f - p->dropout_p);
     const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
+    a.drop_mask = dropout ? p->dropout_mask : nullptr;
     const hipStream_t st = (hipStream_t)stream;
 
     hipError_t e = hipSuccess;

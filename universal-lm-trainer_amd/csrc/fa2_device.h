@@ -393,4 +393,19 @@ __device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, ui
     return (x >> 8) >= thr;
 }
 
+// Dropout keep bits, written by the forward and read by both backward passes
+// instead of evaluating the hash again.  One 32-bit word per (b*H + h,
+// 64-key tile t64, half g2, query q) at word index dmask_word(...): keys in
+// tiles of 64 with dmask_tiles(S) = 2 * ceil(S / 128) tiles (the dK/dV pass
+// reads both 64-key tiles of its 128-key block), queries padded to
+// dmask_rows(S) = S rounded up to 256 (whole query blocks of every pass).
+// Bit 16*kb + 8*hh + e of word g2 is key 64*t64 + 32*kb + 16*hh + 8*(e>>2)
+// + 4*g2 + (e&3): the forward's own register layout, so each lane sets the
+// 32 bits of one word per tile.
+__device__ __forceinline__ int dmask_tiles(int S) { return 2 * ((S + 127) / 128); }
+__device__ __forceinline__ int dmask_rows(int S) { return (S + 255) & ~255; }
+__device__ __forceinline__ int64_t dmask_word(int bh, int S, int t64, int g2, int q) {
+    return ((int64_t)bh * dmask_tiles(S) + t64) * 2 * dmask_rows(S) + (int64_t)g2 * dmask_rows(S) + q;
+}
+
 }  // namespace fa2

@@ -61,8 +61,12 @@ constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <
 // workgroup of slice ks runs the same pipeline over its slice and writes the
 // unnormalised partial result (O accumulator, reference max, row sum) for
 // fwd_combine_kernel instead of O and LSE.
-template <bool CAUSAL, bool DROPOUT, bool SPLIT>
+//
+// DMASK (dropout, no key slices): each lane also stores its tile's 32 keep
+// bits as one word of a.drop_mask (dmask_word layout), for the backward.
+template <bool CAUSAL, bool DROPOUT, bool SPLIT, bool DMASK>
 __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs a) {
+    static_assert(!DMASK || (DROPOUT && !SPLIT && QB == 1 && NST == 4), "keep-bit words: one store per tile");
     // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
     __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
 
@@ -308,6 +312,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         }
         if (DROPOUT) {
             // l sums the un-dropped P; dropout then zeroes / rescales P.
+            uint32_t w = 0;   // DMASK: bit 16*kb + 8*hh + e
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -317,7 +322,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
                         const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
                         const bool keep = dropout_keep(a.seed, qw0 + 32 * qb + c, key, (uint32_t)bh, a.drop_thr);
                         pb[kb][hh][e] = keep ? (_Float16)((float)pb[kb][hh][e] * a.inv_keep) : (_Float16)0.f;
+                        if (DMASK) w |= (uint32_t)keep << (16 * kb + 8 * hh + e);
                     }
+            if (DMASK) {
+                // One store per call: the wave computes this tile, so its
+                // first query (lane c = 0) is below S.
+                const int q = qw0 + 32 * qb + c;
+                if (q < S) a.drop_mask[dmask_word(bh, S, k0 / KT, g2, q)] = w;
+            }
         }
         l[qb] += rs;
     };
@@ -393,8 +405,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // Tile t keeps its scores and P in (s0, p0) for even t and (s1, p1) for
     // odd t.  The end of a tile: tile t+2 landed (tiles up to t+NST-2 are
     // issued), the barrier, and tile t+NST-1 into the stage of tile t-1.
+    // DMASK: the keep-bit store of a computed tile (t <= tlast) is the one
+    // memory operation issued after tile t+2's transfers; it may stay pending.
     auto tile_end = [&](int t) FA2_INLINE {
-        if (NST == 5 && t + 3 < ntiles) vm_wait<4>(); else if (t + 2 < ntiles) vm_wait<0>();
+        if (NST == 5 && t + 3 < ntiles) vm_wait<4>();
+        else if (t + 2 < ntiles) {
+            if (DMASK && t <= tlast) vm_wait<1>(); else vm_wait<0>();
+        }
         lds_barrier();
         if (t + NST - 1 < ntiles) issue(t + NST - 1);
     };
@@ -724,16 +741,22 @@ void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const int nqblk = (a.S + QWG - 1) / QWG;
     const dim3 grid((unsigned)(nqblk * a.B * a.H * (SPLIT ? a.nsplit : 1)));
     const dim3 block(NW * 64);
+    // Keep-bit words only from the unsplit forward (the training path).
+    const bool dmask = !SPLIT && dropout && a.drop_mask != nullptr;
     if (causal) {
-        if (dropout)
-            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT>), grid, block, 0, st, a);
+        if (dmask)
+            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, !SPLIT>), grid, block, 0, st, a);
+        else if (dropout)
+            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, false>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((fwd_kernel<true, false, SPLIT>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<true, false, SPLIT, false>), grid, block, 0, st, a);
     } else {
-        if (dropout)
-            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT>), grid, block, 0, st, a);
+        if (dmask)
+            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, !SPLIT>), grid, block, 0, st, a);
+        else if (dropout)
+            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, false>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((fwd_kernel<false, false, SPLIT>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<false, false, SPLIT, false>), grid, block, 0, st, a);
     }
 }
 

@@ -29,6 +29,8 @@ struct FwdArgs {
     uint32_t seed;       // dropout hash seed
     uint32_t drop_thr;   // keep iff (hash >> 8) >= drop_thr
     float inv_keep;      // 1 / (1 - p)
+    // Dropout keep bits (dmask_word layout) written for the backward, or null.
+    uint32_t *drop_mask;
 };
 
 struct BwdArgs {
@@ -54,6 +56,9 @@ struct BwdArgs {
     uint32_t seed;
     uint32_t drop_thr;
     float inv_keep;
+    // Dropout keep bits the forward wrote (dmask_word layout), or null: the
+    // passes then evaluate the hash themselves.
+    const uint32_t *drop_mask;
 };
 
 struct RopeArgs {

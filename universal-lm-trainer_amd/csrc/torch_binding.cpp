@@ -3,13 +3,16 @@
 // Exposes the reference's four extension ops with their signatures and
 // output conventions (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:386-397):
 //   fa_fwd(q, k, v, dropout_p, causal, softmax_scale, seed)            -> [o, lse]
+// plus fa_fwd_mask (same arguments) -> [o, lse, mask]: with dropout also the
+// keep-bit words (int32, fa2_dropout_mask_bytes), for fa_bwd(..., mask=)
+// to read instead of hashing again (identical gradients);
 // plus, for inference callers (no reference counterpart; fa2_fwd_kv_f16):
 //   fa_fwd_kv(q, k, v, causal, softmax_scale, causal_offset, nsplit=0)  -> [o, lse]
 // with k, v of their own sequence length and key j visible to query i iff
 // j <= i + causal_offset when causal; nsplit slices of the key range
 // (fa2_fwd_kv_split_f16, 0 = chosen here so the grid fills the GPU).
 //   fa_bwd(q, k, v, o, lse, do, dropout_p, causal, softmax_scale, seed,
-//          mode=7)                                                      -> [dq, dk, dv]
+//          mode=7, mask=None)                                           -> [dq, dk, dv]
 //   rope_fwd(q, k, cos, sin)                                            -> [qo, ko]
 //   rope_bwd(dqo, dko, cos, sin, q, k)                                  -> [dq, dk]
 // Inputs are borrowed with their strides; outputs and the backward's
@@ -64,7 +67,8 @@ void check_qkv(const torch::Tensor &q, const torch::Tensor &k, const torch::Tens
 // The forward through fa2_fwd_kv_f16 (s_k = k's length); fa_fwd is the square case.
 std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor &k, const torch::Tensor &v,
                                     double dropout_p, bool causal, double softmax_scale, int64_t seed,
-                                    int64_t causal_offset, const char *op, int64_t nsplit = 1) {
+                                    int64_t causal_offset, const char *op, int64_t nsplit = 1,
+                                    bool want_mask = false) {
     check_dims(q, op);
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     const int64_t B = q.size(0), H = q.size(1), S = q.size(2);
@@ -101,6 +105,13 @@ std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor 
     p.causal = causal ? 1 : 0;
     TORCH_CHECK(k.size(2) <= INT32_MAX && causal_offset >= INT32_MIN && causal_offset <= INT32_MAX,
                 op, ": key length / causal offset out of range");
+    if (want_mask) {   // square forward (fa2_fwd_f16), which alone writes keep bits (none without dropout)
+        auto mask = torch::empty({dropout_p > 0.0 ? (int64_t)(fa2_dropout_mask_bytes(p.B, p.H, p.S) / 4) : 0},
+                                 q.options().dtype(torch::kInt));
+        p.dropout_mask = dropout_p > 0.0 ? reinterpret_cast<uint32_t *>(mask.data_ptr()) : nullptr;
+        check_status(fa2_fwd_f16(&p, current_stream(q)), op);
+        return {o, lse, mask};
+    }
     if (nsplit <= 1) {
         check_status(fa2_fwd_kv_f16(&p, (int32_t)k.size(2), (int32_t)causal_offset, current_stream(q)), op);
     } else {
@@ -117,6 +128,12 @@ std::vector<torch::Tensor> fa_fwd(torch::Tensor q, torch::Tensor k, torch::Tenso
                                   double softmax_scale, int64_t seed) {
     check_qkv(q, k, v);
     return fwd_impl(q, k, v, dropout_p, causal, softmax_scale, seed, 0, "fa_fwd");
+}
+
+std::vector<torch::Tensor> fa_fwd_mask(torch::Tensor q, torch::Tensor k, torch::Tensor v, double dropout_p,
+                                       bool causal, double softmax_scale, int64_t seed) {
+    check_qkv(q, k, v);
+    return fwd_impl(q, k, v, dropout_p, causal, softmax_scale, seed, 0, "fa_fwd_mask", 1, true);
 }
 
 // Key slices for a grid of `wgs` workgroups over `tiles` 64-key tiles: about
@@ -156,7 +173,8 @@ std::vector<torch::Tensor> fa_fwd_kv(torch::Tensor q, torch::Tensor k, torch::Te
 
 std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor o,
                                   torch::Tensor lse, torch::Tensor do_, double dropout_p, bool causal,
-                                  double softmax_scale, int64_t seed, int64_t mode) {
+                                  double softmax_scale, int64_t seed, int64_t mode,
+                                  c10::optional<torch::Tensor> mask) {
     check_qkv(q, k, v);
     TORCH_CHECK(o.sizes() == q.sizes() && do_.sizes() == q.sizes(), "o/do shape mismatch");
     TORCH_CHECK(o.dtype() == torch::kHalf && do_.dtype() == torch::kHalf, "o/do must be fp16");
@@ -165,6 +183,14 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
                 "lse must be fp32 (B,H,S)");
     TORCH_CHECK(mode >= 0 && mode <= 15, "mode must be a bit mask in 0..15");
     check_dims(q, "fa_bwd");
+    if (mask && dropout_p > 0.0) {
+        TORCH_CHECK(mask->is_cuda() && mask->device() == q.device() && mask->dtype() == torch::kInt &&
+                        mask->is_contiguous(),
+                    "fa_bwd: mask must be the contiguous int32 words fa_fwd_mask returned");
+        TORCH_CHECK((size_t)mask->numel() * 4 ==
+                        fa2_dropout_mask_bytes((int32_t)q.size(0), (int32_t)q.size(1), (int32_t)q.size(2)),
+                    "fa_bwd: mask size does not match (B, H, S)");
+    }
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     // The kernels take any (b,h,s) strides; only rows must be contiguous and
     // 16-byte aligned.  lse must have unit stride along s.
@@ -210,6 +236,7 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     p.dropout_p = (float)dropout_p;
     p.seed = (uint32_t)seed;
     p.causal = causal ? 1 : 0;
+    if (mask && dropout_p > 0.0) p.dropout_mask = reinterpret_cast<const uint32_t *>(mask->data_ptr());
     // The workspace is fresh each call, so a dK/dV-only request also computes
     // delta (the reference would read an uninitialised buffer there).
     int32_t m = (int32_t)mode;
@@ -300,13 +327,14 @@ std::vector<torch::Tensor> rope_bwd(torch::Tensor dqo, torch::Tensor dko, torch:
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("fa_fwd", &fa_fwd, "FA2 forward (gfx950 MFMA)");
+    m.def("fa_fwd_mask", &fa_fwd_mask, "FA2 forward that also returns the dropout keep-bit words");
     m.def("fa_fwd_kv", &fa_fwd_kv, "FA2 forward, k/v of their own length (inference)", pybind11::arg("q"),
           pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("causal"), pybind11::arg("softmax_scale"),
           pybind11::arg("causal_offset"), pybind11::arg("nsplit") = 0);
     m.def("fa_bwd", &fa_bwd, "FA2 backward (gfx950 MFMA)", pybind11::arg("q"), pybind11::arg("k"),
           pybind11::arg("v"), pybind11::arg("o"), pybind11::arg("lse"), pybind11::arg("do"),
           pybind11::arg("dropout_p"), pybind11::arg("causal"), pybind11::arg("softmax_scale"),
-          pybind11::arg("seed"), pybind11::arg("mode") = 7);
+          pybind11::arg("seed"), pybind11::arg("mode") = 7, pybind11::arg("mask") = pybind11::none());
     m.def("rope_fwd", &rope_fwd, "fused RoPE forward");
     m.def("rope_bwd", &rope_bwd, "fused RoPE backward");
     m.def("version", []() { return std::string(fa2_version()); });

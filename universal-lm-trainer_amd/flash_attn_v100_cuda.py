@@ -56,6 +56,17 @@ _BUILD_ERROR = None
 # function of (seed, row, col, bh), so saving the seed in ctx is enough.
 _SEED_COUNTER = itertools.count(1)
 
+# With dropout the forward also stores its keep bits (one bit per query/key
+# pair, held until the backward), which the backward then reads instead of
+# hashing again: identical gradients, less backward work.  A call whose words
+# would exceed this many bytes hashes in the backward instead.
+DROPOUT_MASK_MAX_BYTES = int(os.environ.get("FA_V100_DROPOUT_MASK_MAX_BYTES", str(1 << 30)))
+
+
+def dropout_mask_bytes(B, H, S):
+    """Bytes of the keep-bit words of a (B, H, S) call (fa2_dropout_mask_bytes)."""
+    return B * H * (2 * ((S + 127) // 128)) * 2 * ((S + 255) // 256 * 256) * 4
+
 
 def _next_seed():
     """Seed of the next dropout mask (reference flash_attn_v100_cuda.py:32-33)."""
@@ -112,8 +123,12 @@ class _FlashAttnV100Cuda(torch.autograd.Function):
     def forward(ctx, q, k, v, dropout_p, causal, softmax_scale):
         ext = extension()
         seed = _next_seed()
-        o, lse = ext.fa_fwd(q, k, v, float(dropout_p), bool(causal), float(softmax_scale), int(seed))
-        ctx.save_for_backward(q, k, v, o, lse)
+        mask = None
+        if dropout_p > 0 and dropout_mask_bytes(*q.shape[:3]) <= DROPOUT_MASK_MAX_BYTES:
+            o, lse, mask = ext.fa_fwd_mask(q, k, v, float(dropout_p), bool(causal), float(softmax_scale), int(seed))
+        else:
+            o, lse = ext.fa_fwd(q, k, v, float(dropout_p), bool(causal), float(softmax_scale), int(seed))
+        ctx.save_for_backward(q, k, v, o, lse, mask)
         ctx.dropout_p = float(dropout_p)
         ctx.causal = bool(causal)
         ctx.softmax_scale = float(softmax_scale)
@@ -122,13 +137,13 @@ class _FlashAttnV100Cuda(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, o, lse = ctx.saved_tensors
+        q, k, v, o, lse, mask = ctx.saved_tensors
         ext = extension()
         if not hasattr(ext, "fa_bwd"):
             raise NotImplementedError("flash_attn_v100: backward kernel missing from the extension")
         # The kernels read dO through its strides; only rows must be contiguous.
         dq, dk, dv = ext.fa_bwd(q, k, v, o, lse, do if do.stride(3) == 1 else do.contiguous(),
-                                ctx.dropout_p, ctx.causal, ctx.softmax_scale, ctx.seed, 7)
+                                ctx.dropout_p, ctx.causal, ctx.softmax_scale, ctx.seed, 7, mask=mask)
         return dq, dk, dv, None, None, None
 
 
