@@ -49,3 +49,33 @@ def test_train_layout_output_needs_no_copy(fa):
     o2 = fa.flash_attn_v100(q.contiguous(), k.contiguous(), v.contiguous())
     assert o2.is_contiguous()
     assert torch.equal(o, o2)
+
+
+def test_kv_cache_generation_logits_match_sdpa(fa):
+    """Inference drop-in, the way the HF template decodes with a KV cache: an fp16 two-layer decoder
+    runs a 200-token prefill, 24 single-token decode steps, a 40-token chunk and one more step
+    through flash_attn_kvcache; the logits of every step against the same weights on the SDPA path
+    with the bottom-right mask spelled out, in the manner of a logits verification
+    (reference @ None: convert_to_hf.py:440-455), and the last step against a full-sequence forward."""
+    print("case KV-cache generation: 2 layers, B=2, prefill 200, decode steps and a chunk", flush=True)
+    torch.manual_seed(0)
+    mk = dec.Decoder(vocab=1000, n_layers=2, d_ff=512, fa=fa, use_kernel=True).cuda().half().eval()
+    mr = dec.Decoder(vocab=1000, n_layers=2, d_ff=512, fa=None, use_kernel=False).cuda().half().eval()
+    mr.load_state_dict(mk.state_dict())
+    ids = dec.synthetic_ids(2, 300, vocab=1000, seed=3, device="cuda")
+    steps = [(0, 200)] + [(200 + i, 201 + i) for i in range(24)] + [(224, 264), (264, 265)]
+    worst = 0.0
+    with torch.no_grad():
+        ck, cr = mk.new_cache(), mr.new_cache()
+        for a, b in steps:
+            lk = mk.forward_cached(ids[:, a:b], ck, 300)
+            lr = mr.forward_cached(ids[:, a:b], cr, 300)
+            e = rel(lk, lr)
+            worst = max(worst, e)
+            assert e <= 1e-2, f"positions {a}..{b}: logits rel err {e}"
+            assert (lk.argmax(-1) == lr.argmax(-1)).float().mean().item() >= 0.95
+        full = mk.forward(ids[:, :265])
+    e_full = rel(lk[:, -1], full[:, -1])
+    print(f"worst step rel err {worst:.2e}; cached vs full-sequence {e_full:.2e}", flush=True)
+    assert e_full <= 1e-2
+    assert ck[0][0].shape == (2, 12, 265, 64)

@@ -261,3 +261,18 @@ def test_seed_counter_formula(monkeypatch):
     import itertools
     monkeypatch.setattr(fa, "_SEED_COUNTER", itertools.count(1))
     assert [fa._next_seed() for _ in range(3)] == [orc.next_seed(12345, i) for i in (1, 2, 3)]
+
+
+def test_decoder_kv_cache_matches_full_forward_on_cpu():
+    """The decoder's KV-cache inference path (prefill, decode steps, a chunk) on the SDPA fallback
+    equals a full-sequence forward at every position, in fp32 on the CPU."""
+    import fa2_decoder as dec
+    torch.manual_seed(0)
+    m = dec.Decoder(vocab=100, d_model=128, n_heads=2, n_layers=2, d_ff=64, fa=None, use_kernel=False).eval()
+    ids = dec.synthetic_ids(2, 40, vocab=100, seed=2)[:, :40]
+    with torch.no_grad():
+        full = m.forward(ids)
+        cache = m.new_cache()
+        outs = [m.forward_cached(ids[:, a:b], cache, 40) for a, b in ((0, 17), (17, 18), (18, 19), (19, 33), (33, 40))]
+    got = torch.cat(outs, dim=1)
+    assert torch.allclose(got, full, rtol=1e-4, atol=1e-5), (got - full).abs().max()

@@ -53,6 +53,34 @@ class Attention(nn.Module):
             attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         return self.wo(attn.transpose(1, 2).contiguous().view(B, S, D))
 
+    def forward_cached(self, x, cos, sin, cache):
+        """Inference: x holds the last S_new positions of the sequence, cos/sin
+        their RoPE rows, and cache = [k, v] the earlier positions' rotated keys
+        and values ((B,H,S_past,64) each, or None), extended in place.  The
+        queries see every cached key and the causal part of their own: the
+        bottom-right mask an HF-style KV-cache decoder builds
+        (reference @ None: hf_template/modeling_universal_lm.py:228-251),
+        through ``flash_attn_kvcache`` or, on the fallback path, SDPA with
+        that mask spelled out."""
+        B, S, D = x.shape
+        q, k, v = (t.view(B, S, self.h, self.d).transpose(1, 2) for t in self.wqkv(x).chunk(3, dim=-1))
+        fa = self.fa if self.use_kernel else None
+        if fa is not None and fa.rope_can_use(q, k, cos, sin):
+            q, k = fa.rope(q, k, cos, sin)
+        else:
+            c, s = cos[None, None], sin[None, None]
+            q, k = ((t * c + rotate_half(t) * s).to(v.dtype) for t in (q, k))
+        if cache[0] is not None:
+            k, v = torch.cat([cache[0], k], dim=2), torch.cat([cache[1], v], dim=2)
+        cache[0], cache[1] = k, v
+        if fa is not None:
+            attn = fa.flash_attn_kvcache(q, k, v, causal=True)
+        else:
+            Sk = k.shape[2]
+            mask = torch.ones(S, Sk, dtype=torch.bool, device=x.device).tril(Sk - S)
+            attn = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        return self.wo(attn.transpose(1, 2).contiguous().view(B, S, D))
+
 
 class Block(nn.Module):
     def __init__(self, d_model, n_heads, d_ff, fa, use_kernel):
@@ -66,6 +94,11 @@ class Block(nn.Module):
 
     def forward(self, x, cos, sin):
         x = x + self.attn(self.n1(x), cos, sin)
+        h = self.n2(x)
+        return x + self.w2(F.silu(self.w1(h)) * self.w3(h))
+
+    def forward_cached(self, x, cos, sin, cache):
+        x = x + self.attn.forward_cached(self.n1(x), cos, sin, cache)
         h = self.n2(x)
         return x + self.w2(F.silu(self.w1(h)) * self.w3(h))
 
@@ -89,6 +122,22 @@ class Decoder(nn.Module):
         for layer in self.layers:
             x = layer(x, cos, sin)
         return F.linear(self.norm(x), self.emb.weight)  # tied head
+
+    def new_cache(self):
+        return [[None, None] for _ in self.layers]
+
+    def forward_cached(self, ids, cache, max_len):
+        """Logits of the S_new tokens ``ids`` that follow the positions held in
+        ``cache`` (from ``new_cache()``, extended in place): a prefill chunk or
+        one decode step.  ``max_len`` sizes the RoPE tables."""
+        past = 0 if cache[0][0] is None else cache[0][0].shape[2]
+        S = ids.shape[1]
+        cos, sin = wl.rope_tables(max_len, d_model=self.d_model, head_dim=self.head_dim)
+        cos, sin = (t[past:past + S].contiguous().to(ids.device) for t in (cos, sin))
+        x = self.emb(ids)
+        for layer, c in zip(self.layers, cache):
+            x = layer.forward_cached(x, cos, sin, c)
+        return F.linear(self.norm(x), self.emb.weight)
 
     def loss(self, ids):
         logits = self.forward(ids[:, :-1])
