@@ -48,6 +48,7 @@ def parse():
                          "(one query against a 4096-key cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
+    ap.add_argument("--no-dropout", action="store_true", help="skip the dropout p=0.1 timings")
     ap.add_argument("--bwd-mode", type=int, default=7,
                     help="fa_bwd mode of the timed step: 7 = split dQ pass (default), "
                          "15 = fused backward with fp32 dQ atomics")
@@ -149,6 +150,36 @@ def cpu_baseline():
                    f"{c1_ms:.2f} ms median of 10 = {(f1 + b1) / (c1_ms / 1e3) / 1e12:.4f} TFLOP/s; "
                    f"CPU: {cpu_model}"),
     }
+
+
+def dropout_steps(torch, ext, q, k, v, do, scale, stream, step_flops, p=0.1, n=10):
+    """The real-training setting (attention dropout 0.1): fwd+bwd through the
+    binding with the backward hashing again, and with the forward's keep-bit
+    words (fa_fwd_mask) read by the backward instead.  Mean over n steps after
+    two warm-up steps; the binding's output and workspace allocations (from
+    torch's caching allocator) are inside the timed region."""
+    def hashed():
+        o, lse = ext.fa_fwd(q, k, v, p, True, scale, 7)
+        ext.fa_bwd(q, k, v, o, lse, do, p, True, scale, 7, 7)
+
+    def masked():
+        o, lse, m = ext.fa_fwd_mask(q, k, v, p, True, scale, 7)
+        ext.fa_bwd(q, k, v, o, lse, do, p, True, scale, 7, 7, mask=m)
+
+    out = {"p": p, "steps": n}
+    for name, fn in (("hash", hashed), ("keep_bits", masked)):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        out[name] = {"ms_per_step": round(ms, 4), "tflops": round(step_flops / (ms / 1e3) / 1e12, 1)}
+    return out
 
 
 def decoder_step(args, torch, fa):
@@ -413,6 +444,8 @@ def main():
               "fwd_bwd_ms": round(sum(avg.values()), 4),
               "cold_l2": {"ms_per_step": round(cold_ms, 4), "tflops": round(step_flops / (cold_ms / 1e3) / 1e12, 1),
                           "flush_mb": 512, "sample": "median of 10 steps, each after a 512 MB device write"}}
+    if not args.no_dropout:
+        timing["dropout"] = dropout_steps(torch, ext, q, k, v, do, scale, stream, step_flops)
 
     result = {
         "metric": METRIC,
