@@ -113,3 +113,25 @@ def test_autograd_mask_on_off_identical(fa, monkeypatch):
     torch.cuda.synchronize()
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("shape", ["config2", "long"])
+def test_full_size_mask_path_bitwise_equals_hash_path(fa, shape):
+    """At the benchmark shape (B=8 H=12 S=4096, 201 MB of words) and at S=16384 (B=1 H=2): the word
+    path's gradients equal the hash path's bit for bit, so the word addressing holds at full size."""
+    import fa2_workloads as wl
+    say(f"case full-size mask vs hash {shape}")
+    ext = fa.extension()
+    if shape == "config2":
+        q, k, v, do = wl.config_inputs(2, device=DEV)
+    else:
+        q, k, v, do = rand_inputs(1, 2, 16384, seed=3)
+    p, seed = 0.1, 0xD00D
+    o, lse = ext.fa_fwd(q, k, v, p, True, 0.125, seed)
+    o2, lse2, mask = ext.fa_fwd_mask(q, k, v, p, True, 0.125, seed)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    ref = ext.fa_bwd(q, k, v, o, lse, do, p, True, 0.125, seed, 7)
+    got = ext.fa_bwd(q, k, v, o, lse, do, p, True, 0.125, seed, 7, mask=mask)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dQ", "dK", "dV"), got, ref):
+        assert torch.equal(a, b), f"{name} differs"
