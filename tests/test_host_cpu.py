@@ -276,3 +276,15 @@ def test_decoder_kv_cache_matches_full_forward_on_cpu():
         outs = [m.forward_cached(ids[:, a:b], cache, 40) for a, b in ((0, 17), (17, 18), (18, 19), (19, 33), (33, 40))]
     got = torch.cat(outs, dim=1)
     assert torch.allclose(got, full, rtol=1e-4, atol=1e-5), (got - full).abs().max()
+
+
+def test_python_mask_size_matches_c_abi(monkeypatch):
+    """The autograd wrapper sizes the keep-bit words with the C ABI's formula, and a malformed
+    FA_V100_DROPOUT_MASK_MAX_BYTES falls back to the default cap instead of failing the import."""
+    lib = capi.load()
+    for B, H, S in ((1, 1, 1), (2, 3, 257), (8, 12, 4096), (1, 2, 16384), (3, 5, 1000)):
+        assert fa.dropout_mask_bytes(B, H, S) == lib.fa2_dropout_mask_bytes(B, H, S), (B, H, S)
+    monkeypatch.setenv("FA_V100_DROPOUT_MASK_MAX_BYTES", "lots")
+    assert fa._mask_cap() == 1 << 30
+    monkeypatch.setenv("FA_V100_DROPOUT_MASK_MAX_BYTES", "0")
+    assert fa._mask_cap() == 0

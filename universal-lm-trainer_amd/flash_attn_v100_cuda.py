@@ -60,7 +60,15 @@ _SEED_COUNTER = itertools.count(1)
 # pair, held until the backward), which the backward then reads instead of
 # hashing again: identical gradients, less backward work.  A call whose words
 # would exceed this many bytes hashes in the backward instead.
-DROPOUT_MASK_MAX_BYTES = int(os.environ.get("FA_V100_DROPOUT_MASK_MAX_BYTES", str(1 << 30)))
+def _mask_cap(default=1 << 30):
+    text = os.environ.get("FA_V100_DROPOUT_MASK_MAX_BYTES", "")
+    try:
+        return int(text) if text.strip() else default
+    except ValueError:   # a malformed setting must not break the import (and train.py with it)
+        return default
+
+
+DROPOUT_MASK_MAX_BYTES = _mask_cap()
 
 
 def dropout_mask_bytes(B, H, S):
