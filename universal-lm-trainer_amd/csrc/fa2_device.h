@@ -378,7 +378,9 @@ __device__ __forceinline__ float sum_h8(h8 v, float acc) {
 // seed*0x9E3779B1 ^ (row+1)*0x85EBCA6B ^ (col+1)*0xC2B2AE35 ^ (bh+1)*0x27D4EB2F,
 // keep iff (h >> 8) * 2^-24 >= p.  Since (h >> 8) < 2^24 that fp32 compare is
 // exact and equals (h >> 8) >= thr with thr = ceil(p * 2^24), computed on the
-// host, so the kernels stay in integer arithmetic.
+// host, so the kernels stay in integer arithmetic.  p < 1 gives thr < 2^24,
+// so (h >> 8) >= thr is h >= thr * 2^8, a compare against a loop-invariant
+// bound with no shift per element.
 __device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, uint32_t bh,
                                              uint32_t thr) {
     uint32_t x = seed * 0x9E3779B1u;
@@ -390,7 +392,7 @@ __device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, ui
     x ^= x >> 15;
     x *= 0x846ca68bu;
     x ^= x >> 16;
-    return (x >> 8) >= thr;
+    return x >= (thr << 8);
 }
 
 // Dropout keep bits, written by the forward and read by both backward passes
