@@ -333,7 +333,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         if (!DROPOUT) return p * g;
         const int key = t * DQ_KT + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
         const bool keep = DMASK ? ((mw >> (16 * kb + r)) & 1u) != 0
-                                : dropout_keep(a.seed, qw0 + 32 * qb + c, key, (uint32_t)bh, a.drop_thr);
+                                : dropout_keep_hashed(dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh) ^
+                                                          dropout_col_term(key),
+                                                      a.drop_thr);
         g = keep ? g * a.inv_keep : 0.f;
         return p * (g - dl[qb]);
     };
@@ -990,6 +992,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     typedef uint32_t u4v __attribute__((ext_vector_type(4)));
     const int kbit = 16 * (wave & 1) + 8 * ((c >> 4) & 1) + 4 * ((c >> 3) & 1) + (c & 3);
     const int dm_run = 2 * (wave >> 1) + ((c >> 2) & 1);
+    // Hash path: the seed, head and key terms of this lane's key, once.
+    const uint32_t hcol = DROPOUT && !DMASK ? dropout_col_part(a.seed, key, (uint32_t)bh) : 0u;
     auto pds = [&](float sv, float g, float l, float dl, int q, uint32_t mw, float &pd, float &ds) FA2_INLINE {
         if (FOLD) {
             pd = __builtin_amdgcn_exp2f(sv * scale2);
@@ -998,7 +1002,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         }
         const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -l));
         if (DROPOUT) {
-            const bool keep = DMASK ? ((mw >> kbit) & 1u) != 0 : dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
+            const bool keep = DMASK ? ((mw >> kbit) & 1u) != 0
+                                    : dropout_keep_hashed(hcol ^ dropout_row_term(q), a.drop_thr);
             pd = keep ? p * a.inv_keep : 0.f;
             ds = pd * g - p * dl;
         } else {

@@ -381,18 +381,29 @@ __device__ __forceinline__ float sum_h8(h8 v, float acc) {
 // host, so the kernels stay in integer arithmetic.  p < 1 gives thr < 2^24,
 // so (h >> 8) >= thr is h >= thr * 2^8, a compare against a loop-invariant
 // bound with no shift per element.
-__device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, uint32_t bh,
-                                             uint32_t thr) {
-    uint32_t x = seed * 0x9E3779B1u;
-    x ^= (uint32_t)(row + 1) * 0x85EBCA6Bu;
-    x ^= (uint32_t)(col + 1) * 0xC2B2AE35u;
-    x ^= (bh + 1u) * 0x27D4EB2Fu;
+// The hash input is (seed and head terms) ^ row term ^ column term.  A lane
+// that keeps one query (or one key) over many elements computes that part once
+// (dropout_row_part / dropout_col_part) and adds the other term per element.
+__device__ __forceinline__ uint32_t dropout_row_term(int row) { return (uint32_t)(row + 1) * 0x85EBCA6Bu; }
+__device__ __forceinline__ uint32_t dropout_col_term(int col) { return (uint32_t)(col + 1) * 0xC2B2AE35u; }
+__device__ __forceinline__ uint32_t dropout_row_part(uint32_t seed, int row, uint32_t bh) {
+    return (seed * 0x9E3779B1u) ^ dropout_row_term(row) ^ ((bh + 1u) * 0x27D4EB2Fu);
+}
+__device__ __forceinline__ uint32_t dropout_col_part(uint32_t seed, int col, uint32_t bh) {
+    return (seed * 0x9E3779B1u) ^ dropout_col_term(col) ^ ((bh + 1u) * 0x27D4EB2Fu);
+}
+// Keep decision from the full hash input x.
+__device__ __forceinline__ bool dropout_keep_hashed(uint32_t x, uint32_t thr) {
     x ^= x >> 16;
     x *= 0x7feb352du;
     x ^= x >> 15;
     x *= 0x846ca68bu;
     x ^= x >> 16;
     return x >= (thr << 8);
+}
+__device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, uint32_t bh,
+                                             uint32_t thr) {
+    return dropout_keep_hashed(dropout_row_part(seed, row, bh) ^ dropout_col_term(col), thr);
 }
 
 // Dropout keep bits, written by the forward and read by both backward passes

@@ -312,7 +312,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         }
         if (DROPOUT) {
             // l sums the un-dropped P; dropout then zeroes / rescales P.
+            // The keep decision selects the multiplier (1/(1-p) or 0), not
+            // the product: the same values, in fewer instructions.
             uint32_t w = 0;   // DMASK: bit 16*kb + 8*hh + e
+            const uint32_t hrow = dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -320,8 +323,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
-                        const bool keep = dropout_keep(a.seed, qw0 + 32 * qb + c, key, (uint32_t)bh, a.drop_thr);
-                        pb[kb][hh][e] = keep ? (_Float16)((float)pb[kb][hh][e] * a.inv_keep) : (_Float16)0.f;
+                        const bool keep = dropout_keep_hashed(hrow ^ dropout_col_term(key), a.drop_thr);
+                        const float m = keep ? a.inv_keep : 0.f;
+                        pb[kb][hh][e] = (_Float16)((float)pb[kb][hh][e] * m);
                         if (DMASK) w |= (uint32_t)keep << (16 * kb + 8 * hh + e);
                     }
             if (DMASK) {
