@@ -312,22 +312,41 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         }
         if (DROPOUT) {
             // l sums the un-dropped P; dropout then zeroes / rescales P.
-            // The keep decision selects the multiplier (1/(1-p) or 0), not
-            // the product: the same values, in fewer instructions.
+            // The keep decision selects the multiplier m = 1/(1-p) or 0, and
+            // each packed fp16 pair of P is scaled in place by two mixed-
+            // precision FMAs, v_fma_mixlo_f16 / v_fma_mixhi_f16: P * m + 0 in
+            // fp32 with P read as fp16 (op_sel_hi bit 1 of source 0; op_sel
+            // bit 1 picks its high half) and m as fp32, the result rounded to
+            // fp16 into the low / high half.  That is one instruction per
+            // element instead of a widen, a multiply and half a repack.
             uint32_t w = 0;   // DMASK: bit 16*kb + 8*hh + e
             const uint32_t hrow = dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
+                for (int hh = 0; hh < 2; ++hh) {
+                    typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+                    u4x pk = __builtin_bit_cast(u4x, pb[kb][hh]);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
-                        const bool keep = dropout_keep_hashed(hrow ^ dropout_col_term(key), a.drop_thr);
-                        const float m = keep ? a.inv_keep : 0.f;
-                        pb[kb][hh][e] = (_Float16)((float)pb[kb][hh][e] * m);
-                        if (DMASK) w |= (uint32_t)keep << (16 * kb + 8 * hh + e);
+                    for (int e2 = 0; e2 < 4; ++e2) {
+                        float m[2];
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const int e = 2 * e2 + j;
+                            const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
+                            const bool keep = dropout_keep_hashed(hrow ^ dropout_col_term(key), a.drop_thr);
+                            m[j] = keep ? a.inv_keep : 0.f;
+                            if (DMASK) w |= (uint32_t)keep << (16 * kb + 8 * hh + e);
+                        }
+                        uint32_t r;
+                        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pk[e2]), "v"(m[0]));
+                        asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                            : "+v"(r)
+                            : "v"(pk[e2]), "v"(m[1]));
+                        pk[e2] = r;
                     }
+                    pb[kb][hh] = __builtin_bit_cast(h8, pk);
+                }
             if (DMASK) {
                 // One store per call: the wave computes this tile, so its
                 // first query (lane c = 0) is below S.
