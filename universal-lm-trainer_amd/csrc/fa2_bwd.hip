@@ -332,12 +332,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -lse2[qb]));
         if (!DROPOUT) return p * g;
         const int key = t * DQ_KT + 32 * kb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-        const bool keep = DMASK ? ((mw >> (16 * kb + r)) & 1u) != 0
-                                : dropout_keep_hashed(dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh) ^
-                                                          dropout_col_term(key),
-                                                      a.drop_thr);
-        g = keep ? g * a.inv_keep : 0.f;
-        return p * (g - dl[qb]);
+        // The keep decision selects the multiplier 1/(1-p) or 0 (from the
+        // word: keep_multiplier; from the hash: a select), the same form on
+        // both paths so that they give the same bits.
+        const float m = DMASK ? keep_multiplier(mw, 16 * kb + r, a.inv_keep)
+                              : (dropout_keep_hashed(dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh) ^
+                                                         dropout_col_term(key),
+                                                     a.drop_thr)
+                                     ? a.inv_keep
+                                     : 0.f);
+        return p * (g * m - dl[qb]);
     };
     auto keep_word = [&](int t, int qb) FA2_INLINE -> uint32_t {
         return DMASK ? sMQ[DMASK ? stage_of(t) : 0][wave][g2][32 * qb + c] : 0u;

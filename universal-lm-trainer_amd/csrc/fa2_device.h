@@ -406,6 +406,13 @@ __device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, ui
     return dropout_keep_hashed(dropout_row_part(seed, row, bh) ^ dropout_col_term(col), thr);
 }
 
+// 1/(1-p) if bit `bit` of the keep word w is set, else 0: the bit sign-
+// extended (0 or all ones) masks the multiplier's bits, with no compare.
+__device__ __forceinline__ float keep_multiplier(uint32_t w, int bit, float inv_keep) {
+    const uint32_t sel = (uint32_t)((int32_t)(w << (31 - bit)) >> 31);
+    return __builtin_bit_cast(float, sel & __builtin_bit_cast(uint32_t, inv_keep));
+}
+
 // Dropout keep bits, written by the forward and read by both backward passes
 // instead of evaluating the hash again.  One 32-bit word per (b*H + h,
 // 64-key tile t64, half g2, query q) at word index dmask_word(...): keys in
