@@ -76,7 +76,7 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
  * the forward only (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:40-364).
  * Word layout, per (b, h), 64-key tile t (< 2*ceil(S/128)), half g (0, 1) and
  * query i (< R = S rounded up to 256): word ((b*H + h)*T + t)*2*R + g*R + i,
- * T = 2*ceil(S/128); its bit 16*kb + 8*hh + e is key
+ * T = 2*ceil(S/128); its bit 31 - (16*kb + 8*hh + e) is key
  * 64*t + 32*kb + 16*hh + 8*(e/4) + 4*g + e%4 (kb, hh in 0..1, e in 0..7). */
 size_t fa2_dropout_mask_bytes(int32_t B, int32_t H, int32_t S);
 

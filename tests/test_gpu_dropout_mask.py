@@ -32,14 +32,14 @@ def rand_inputs(B, H, S, seed):
 
 def mask_bits(words, B, H, S):
     """[B*H, S, S] keep bits (query row, key col) read out of the words: word
-    ((bh*T + t)*2 + g)*R + i, bit 16*kb + 8*hh + e holds key
+    ((bh*T + t)*2 + g)*R + i, bit 31 - (16*kb + 8*hh + e) holds key
     64*t + 32*kb + 16*hh + 8*(e//4) + 4*g + e%4 (T = 2*ceil(S/128), R = S rounded up to 256)."""
     T, R = 2 * ((S + 127) // 128), (S + 255) // 256 * 256
     w = words.reshape(B * H, T, 2, R)[:, :, :, :S]
     j = np.arange(S)
     t, r = j // 64, j % 64
     kb, hh, e_hi, g, e_lo = r // 32, (r // 16) % 2, (r // 8) % 2, (r // 4) % 2, r % 4
-    bit = 16 * kb + 8 * hh + 4 * e_hi + e_lo
+    bit = 31 - (16 * kb + 8 * hh + 4 * e_hi + e_lo)
     sel = w[:, t, g, :]                                  # [BH, S keys, S rows]
     return ((sel >> bit[None, :, None].astype(np.uint32)) & 1).transpose(0, 2, 1).astype(bool)
 

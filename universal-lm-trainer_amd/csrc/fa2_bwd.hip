@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     // dS of element r of unit (t, kb, qb) from its score and dP value.
     // (Without dropout g is dP - delta already.)
     // DMASK: mw is the unit's keep word (query qw0 + 32*qb + c, tile t, half
-    // g2), whose bit 16*kb + r is element r's.
+    // g2), whose bit 31 - (16*kb + r) is element r's.
     auto ds_of = [&](float sv, float g, int t, int kb, int qb, int r, uint32_t mw) FA2_INLINE {
         const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -lse2[qb]));
         if (!DROPOUT) return p * g;
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         // The keep decision selects the multiplier 1/(1-p) or 0 (from the
         // word: keep_multiplier; from the hash: a select), the same form on
         // both paths so that they give the same bits.
-        const float m = DMASK ? keep_multiplier(mw, 16 * kb + r, a.inv_keep)
+        const float m = DMASK ? keep_multiplier(mw, 31 - (16 * kb + r), a.inv_keep)
                               : (dropout_keep_hashed(dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh) ^
                                                          dropout_col_term(key),
                                                      a.drop_thr)
@@ -994,7 +994,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     // DMASK: mw is the keep word of the element's query row, whose bit kbit
     // is this lane's key (run dm_run of the tile's words).
     typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-    const int kbit = 16 * (wave & 1) + 8 * ((c >> 4) & 1) + 4 * ((c >> 3) & 1) + (c & 3);
+    const int kbit = 31 - (16 * (wave & 1) + 8 * ((c >> 4) & 1) + 4 * ((c >> 3) & 1) + (c & 3));
     const int dm_run = 2 * (wave >> 1) + ((c >> 2) & 1);
     // Hash path: the seed, head and key terms of this lane's key, once.
     const uint32_t hcol = DROPOUT && !DMASK ? dropout_col_part(a.seed, key, (uint32_t)bh) : 0u;

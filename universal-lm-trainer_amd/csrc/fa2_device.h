@@ -419,9 +419,9 @@ __device__ __forceinline__ float keep_multiplier(uint32_t w, int bit, float inv_
 // tiles of 64 with dmask_tiles(S) = 2 * ceil(S / 128) tiles (the dK/dV pass
 // reads both 64-key tiles of its 128-key block), queries padded to
 // dmask_rows(S) = S rounded up to 256 (whole query blocks of every pass).
-// Bit 16*kb + 8*hh + e of word g2 is key 64*t64 + 32*kb + 16*hh + 8*(e>>2)
-// + 4*g2 + (e&3): the forward's own register layout, so each lane sets the
-// 32 bits of one word per tile.
+// Bit 31 - (16*kb + 8*hh + e) of word g2 is key 64*t64 + 32*kb + 16*hh +
+// 8*(e>>2) + 4*g2 + (e&3): the forward's own register order, shifted into
+// the word element by element, so each lane builds one word per tile.
 __device__ __forceinline__ int dmask_tiles(int S) { return 2 * ((S + 127) / 128); }
 __device__ __forceinline__ int dmask_rows(int S) { return (S + 255) & ~255; }
 __device__ __forceinline__ int64_t dmask_word(int bh, int S, int t64, int g2, int q) {

@@ -312,14 +312,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         }
         if (DROPOUT) {
             // l sums the un-dropped P; dropout then zeroes / rescales P.
-            // The keep decision selects the multiplier m = 1/(1-p) or 0, and
+            // The keep decision selects the multiplier m = -1/(1-p) or +0, and
             // each packed fp16 pair of P is scaled in place by two mixed-
-            // precision FMAs, v_fma_mixlo_f16 / v_fma_mixhi_f16: P * m + 0 in
-            // fp32 with P read as fp16 (op_sel_hi bit 1 of source 0; op_sel
-            // bit 1 picks its high half) and m as fp32, the result rounded to
-            // fp16 into the low / high half.  That is one instruction per
-            // element instead of a widen, a multiply and half a repack.
-            uint32_t w = 0;   // DMASK: bit 16*kb + 8*hh + e
+            // precision FMAs, v_fma_mixlo_f16 / v_fma_mixhi_f16: (-P) * m + 0
+            // in fp32 with P read as fp16 (op_sel_hi bit 1 of source 0; op_sel
+            // bit 1 picks its high half; "-" negates it) and m as fp32, the
+            // result rounded to fp16 into the low / high half.  That is one
+            // instruction per element instead of a widen, a multiply and half
+            // a repack.  m's sign bit is the keep bit: DMASK shifts it into
+            // the word (one funnel shift, v_alignbit_b32, per element), so
+            // element 16*kb + 8*hh + e lands on bit 31 - (16*kb + 8*hh + e).
+            uint32_t w = 0;
             const uint32_t hrow = dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -335,12 +338,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
                             const int e = 2 * e2 + j;
                             const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
                             const bool keep = dropout_keep_hashed(hrow ^ dropout_col_term(key), a.drop_thr);
-                            m[j] = keep ? a.inv_keep : 0.f;
-                            if (DMASK) w |= (uint32_t)keep << (16 * kb + 8 * hh + e);
+                            m[j] = keep ? -a.inv_keep : 0.f;
+                            if (DMASK) w = (w << 1) | (__builtin_bit_cast(uint32_t, m[j]) >> 31);
                         }
                         uint32_t r;
-                        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pk[e2]), "v"(m[0]));
-                        asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                        asm("v_fma_mixlo_f16 %0, -%1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pk[e2]), "v"(m[0]));
+                        asm("v_fma_mixhi_f16 %0, -%1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
                             : "+v"(r)
                             : "v"(pk[e2]), "v"(m[1]));
                         pk[e2] = r;
