@@ -286,6 +286,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // After P of tile k0 (K tile in `stage`) was formed with partial sum rs:
     // the cold path (scores recomputed from the K tile, so no score register
     // has to outlive P), dropout, and the running sum.
+    uint32_t wpend = 0;   // DMASK: the keep word of the tile being finished
     auto softmax_tail = [&](int qb, int k0, int stage, h8(&pb)[2][2], float rs) FA2_INLINE {
         if (__any(!(rs <= P_SUM_LIMIT))) {
             FA2_COLD_BRANCH();
@@ -350,12 +351,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
                     }
                     pb[kb][hh] = __builtin_bit_cast(h8, pk);
                 }
-            if (DMASK) {
-                // One store per call: the wave computes this tile, so its
-                // first query (lane c = 0) is below S.
-                const int q = qw0 + 32 * qb + c;
-                if (q < S) a.drop_mask[dmask_word(bh, S, k0 / KT, g2, q)] = w;
-            }
+            if (DMASK) wpend = w;   // stored by tile_end
         }
         l[qb] += rs;
     };
@@ -431,15 +427,19 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // Tile t keeps its scores and P in (s0, p0) for even t and (s1, p1) for
     // odd t.  The end of a tile: tile t+2 landed (tiles up to t+NST-2 are
     // issued), the barrier, and tile t+NST-1 into the stage of tile t-1.
-    // DMASK: the keep-bit store of a computed tile (t <= tlast) is the one
-    // memory operation issued after tile t+2's transfers; it may stay pending.
+    // DMASK: a computed tile's (t <= tlast) keep word is stored here, after
+    // the wait, the barrier and the next tile's transfers, so the count-based
+    // wait stays vmcnt(0) -- it needs no ordering between loads and stores --
+    // and the store has a whole step to complete before the next one.
     auto tile_end = [&](int t) FA2_INLINE {
         if (NST == 5 && t + 3 < ntiles) vm_wait<4>();
-        else if (t + 2 < ntiles) {
-            if (DMASK && t <= tlast) vm_wait<1>(); else vm_wait<0>();
-        }
+        else if (t + 2 < ntiles) vm_wait<0>();
         lds_barrier();
         if (t + NST - 1 < ntiles) issue(t + NST - 1);
+        if (DMASK && t <= tlast) {
+            const int q = qw0 + c;   // QB == 1
+            if (q < S) a.drop_mask[dmask_word(bh, S, kbase / KT + t, g2, q)] = wpend;
+        }
     };
     // Steady state (1 <= t < tsteady): no masking -- the tile is below this
     // wave's diagonal and not the last one -- and every group present.
