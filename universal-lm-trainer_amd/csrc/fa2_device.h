@@ -407,9 +407,10 @@ __device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, ui
 }
 
 // 1/(1-p) if bit `bit` of the keep word w is set, else 0: the bit sign-
-// extended (0 or all ones) masks the multiplier's bits, with no compare.
+// extended (v_bfe_i32: 0 or all ones) masks the multiplier's bits, with no
+// compare.
 __device__ __forceinline__ float keep_multiplier(uint32_t w, int bit, float inv_keep) {
-    const uint32_t sel = (uint32_t)((int32_t)(w << (31 - bit)) >> 31);
+    const uint32_t sel = (uint32_t)__builtin_amdgcn_sbfe((int)w, bit, 1);
     return __builtin_bit_cast(float, sel & __builtin_bit_cast(uint32_t, inv_keep));
 }
 
