@@ -1006,9 +1006,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         }
         const float p = __builtin_amdgcn_exp2f(fmaf(sv, scale2, -l));
         if (DROPOUT) {
-            const bool keep = DMASK ? ((mw >> kbit) & 1u) != 0
-                                    : dropout_keep_hashed(hcol ^ dropout_row_term(q), a.drop_thr);
-            pd = keep ? p * a.inv_keep : 0.f;
+            if (DMASK) {
+                pd = p * keep_multiplier(mw, kbit, a.inv_keep);   // p >= 0: p * 0 = +0, as the select
+            } else {
+                const bool keep = dropout_keep_hashed(hcol ^ dropout_row_term(q), a.drop_thr);
+                pd = keep ? p * a.inv_keep : 0.f;
+            }
             ds = pd * g - p * dl;
         } else {
             pd = p;
