@@ -95,11 +95,81 @@ def read_traffic(kernel):
     return None
 
 
+class ClockSampler:
+    """Samples the GPU's graphics clock from the SMU metrics table (amdsmi
+    gpu_metrics: current_gfxclks per XCD where reported, else current_gfxclk)
+    every `period` seconds on a background thread while a timed region runs;
+    the median of the samples is the sustained clock reported beside the
+    result.  Unavailable metrics leave the report empty, never the bench."""
+
+    def __init__(self, torch, period=0.001):
+        import threading
+        self.period, self.samples, self.error, self.h = period, [], None, None
+        self._stop = threading.Event()
+        self._thread = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            handles = amdsmi.amdsmi_get_processor_handles()
+            want = getattr(torch.cuda.get_device_properties(0), "pci_bus_id", None)
+            self.h = handles[0]
+            for h in handles:
+                bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)
+                if want is not None and int(bdf.split(":")[1], 16) == int(want):
+                    self.h = h
+            self._amdsmi = amdsmi
+            self._read()
+        except Exception as e:  # noqa: BLE001 -- any failure only disables the clock report
+            self.error, self.h = f"{type(e).__name__}: {e}", None
+
+    def _read(self):
+        m = self._amdsmi.amdsmi_get_gpu_metrics_info(self.h)
+        vals = [c for c in (m.get("current_gfxclks") or []) if isinstance(c, int) and 0 < c < 0xFFFF]
+        if not vals and isinstance(m.get("current_gfxclk"), int) and 0 < m["current_gfxclk"] < 0xFFFF:
+            vals = [m["current_gfxclk"]]
+        return sum(vals) / len(vals) if vals else None
+
+    def _run(self):
+        while not self._stop.wait(self.period):
+            try:
+                v = self._read()
+            except Exception as e:  # noqa: BLE001
+                self.error = f"{type(e).__name__}: {e}"
+                return
+            if v is not None:
+                self.samples.append(v)
+
+    def __enter__(self):
+        import threading
+        if self.h is not None:
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join(timeout=1.0)
+
+    def report(self):
+        if not self.samples:
+            return {"mhz_median": None, "samples": 0,
+                    "source": f"amdsmi gpu_metrics unavailable ({self.error or 'no samples'})"}
+        return {"mhz_median": round(statistics.median(self.samples), 1),
+                "mhz_min": round(min(self.samples), 1), "mhz_max": round(max(self.samples), 1),
+                "samples": len(self.samples),
+                "source": "amdsmi gpu_metrics current_gfxclk(s) (mean over XCDs), sampled every "
+                          f"{self.period * 1e3:.0f} ms during the timed steps"}
+
+
 def cpu_baseline():
     """The reference's CPU path (train.py:1956-1961): SDPA fwd + .backward(dO)
-    in fp32 with the default CPU dispatch, on a bounded sample."""
+    in fp32, timed with the default CPU dispatch (what the reference runs) and
+    with SDPBackend.MATH (the parity oracle), forward and backward apart, on a
+    bounded sample: configuration 1 in full and a B=1 slice of configuration 2."""
     import torch
     import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
     import fa2_workloads as wl
     cores = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS")
@@ -107,29 +177,39 @@ def cpu_baseline():
         cores = min(cores, int(omp))
     torch.set_num_threads(cores)
 
-    def step(q, k, v, do):
+    def step(q, k, v, do, backend):
         q, k, v = (t.detach().requires_grad_(True) for t in (q, k, v))
-        o = F.scaled_dot_product_attention(q, k, v, attn_mask=None, dropout_p=0.0, is_causal=True)
-        o.backward(do)
-
-    # configuration 1 in full: median of 10 after 2 warm-ups
-    q, k, v, do = wl.config_inputs(1)
-    for _ in range(2):
-        step(q, k, v, do)
-    ts = []
-    for _ in range(10):
         t0 = time.perf_counter()
-        step(q, k, v, do)
-        ts.append(time.perf_counter() - t0)
-    c1_ms = statistics.median(ts) * 1e3
+        if backend is None:
+            o = F.scaled_dot_product_attention(q, k, v, attn_mask=None, dropout_p=0.0, is_causal=True)
+        else:
+            with sdpa_kernel(backend):
+                o = F.scaled_dot_product_attention(q, k, v, attn_mask=None, dropout_p=0.0, is_causal=True)
+        t1 = time.perf_counter()
+        o.backward(do)
+        t2 = time.perf_counter()
+        return (t1 - t0) * 1e3, (t2 - t1) * 1e3
+
+    def timed(inputs, backend, warm, n):
+        for _ in range(warm):
+            step(*inputs, backend)
+        runs = [step(*inputs, backend) for _ in range(n)]
+        fwd = statistics.median(r[0] for r in runs)
+        bwd = statistics.median(r[1] for r in runs)
+        tot = statistics.median(r[0] + r[1] for r in runs)
+        return {"fwd_ms": round(fwd, 3), "bwd_ms": round(bwd, 3), "fwd_bwd_ms": round(tot, 3)}
+
+    c1 = wl.config_inputs(1)
+    c2 = tuple(t[:1].float() for t in wl.config_inputs(2))
     f1, b1 = wl.causal_flops(2, 4, 256)
-    # configuration-2 shape, B=1 slice (fp32), one warm-up + one timed run; scaled by B
-    q, k, v, do = (t[:1].float() for t in wl.config_inputs(2))
-    step(q, k, v, do)
-    t0 = time.perf_counter()
-    step(q, k, v, do)
-    c2_s = time.perf_counter() - t0
     f2, b2 = wl.causal_flops(1, 12, 4096)
+    out = {}
+    for name, backend in (("default", None), ("math", SDPBackend.MATH)):
+        r1 = timed(c1, backend, 2, 10)
+        r2 = timed(c2, backend, 1, 1)
+        r1["tflops"] = round((f1 + b1) / (r1["fwd_bwd_ms"] / 1e3) / 1e12, 5)
+        r2["tflops"] = round((f2 + b2) / (r2["fwd_bwd_ms"] / 1e3) / 1e12, 5)
+        out[name] = {"config1": r1, "config2_b1_slice": r2}
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -138,17 +218,19 @@ def cpu_baseline():
                 break
     except OSError:
         pass
+    d2 = out["default"]["config2_b1_slice"]
     return {
-        "value": round((f2 + b2) / c2_s / 1e12, 5),
+        "value": d2["tflops"],
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "reference",
         "sample": (f"reference fallback F.scaled_dot_product_attention(is_causal=True) fwd+.backward, fp32, "
                    f"default CPU dispatch, torch {torch.__version__}; B=1 slice of config 2 "
-                   f"(H=12 S=4096 D=64): {c2_s * 1e3:.0f} ms per fwd+bwd, value = that slice's causal "
-                   f"flops / time (whole config 2 = 8x the time); config 1 (B=2 H=4 S=256): "
-                   f"{c1_ms:.2f} ms median of 10 = {(f1 + b1) / (c1_ms / 1e3) / 1e12:.4f} TFLOP/s; "
-                   f"CPU: {cpu_model}"),
+                   f"(H=12 S=4096 D=64): {d2['fwd_bwd_ms']:.0f} ms per fwd+bwd (fwd {d2['fwd_ms']:.0f}, "
+                   f"bwd {d2['bwd_ms']:.0f}), value = that slice's causal flops / time (whole config 2 = "
+                   f"8x the time); config 1 (B=2 H=4 S=256) in full, median of 10; the same again with "
+                   f"SDPBackend.MATH (the parity oracle) under 'backends'; CPU: {cpu_model}"),
+        "backends": out,
     }
 
 
@@ -193,6 +275,19 @@ def decoder_step(args, torch, fa):
     import fa2_decoder as dec
     B, S, L = 4, 4096, 10
     ext = fa.extension()
+    parity = None
+    if not args.no_parity:
+        # The same weights through the kernel path and through eager RoPE + SDPA math
+        # fp32 attention: loss within 1e-3 relative, every gradient within 1e-2.
+        lk, lr, errs = dec.compare_training_step(fa, B=B, S=S, n_layers=L)
+        worst = max(errs, key=errs.get)
+        parity = {"loss_kernel": lk, "loss_reference": lr, "loss_rel": abs(lk - lr) / abs(lr),
+                  "worst_grad": worst, "worst_grad_rel": errs[worst]}
+        ok = parity["loss_rel"] < 1e-3 and errs[worst] < 1e-2
+        print(f"parity {parity} {'ok' if ok else 'FAILED'}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        if not ok:
+            raise SystemExit("parity gate failed: no performance report")
     torch.manual_seed(0)
     model = dec.Decoder(n_layers=L, fa=fa).cuda()
     opt = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.1, betas=(0.9, 0.95), fused=True)
@@ -243,17 +338,23 @@ def decoder_step(args, torch, fa):
         step()
     torch.cuda.synchronize()
     rec[0] = True
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        loss = step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    sev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    clock = ClockSampler(torch)
+    with clock:
+        t0 = time.perf_counter()
+        sev[0].record()
+        for i in range(args.steps):
+            loss = step()
+            sev[i + 1].record()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
     rec[0] = False
     attn_ms = sum(a.elapsed_time(b) for a, b in spans) / args.steps
     assert len(spans) == 2 * L * args.steps, len(spans)
     attn_flops = dec.step_flops_attention(B, S, n_layers=L)
     value = attn_flops / (attn_ms / 1e3) / 1e12
-    ms_per_step = elapsed / args.steps * 1e3
+    step_ms = [sev[i].elapsed_time(sev[i + 1]) for i in range(args.steps)]
+    ms_per_step = statistics.median(step_ms)
     return {
         "metric": METRIC,
         "value": round(value, 2),
@@ -268,10 +369,14 @@ def decoder_step(args, torch, fa):
                                f"value = attention fwd+bwd rate inside the step",
                    "B": B, "S": S, "layers": L, "bwd_mode": args.bwd_mode},
         "step": {"tokens_per_s": round(B * S / (ms_per_step / 1e3), 1),
+                 "ms_median_events": round(ms_per_step, 3),
+                 "ms_wall_mean": round(elapsed / args.steps * 1e3, 3),
                  "attention_ms_per_step": round(attn_ms, 3),
                  "attention_share": round(attn_ms / ms_per_step, 4),
                  "approx_model_tflops": round(dec.approx_step_flops(B, S) / (ms_per_step / 1e3) / 1e12, 1),
                  "last_loss": round(float(loss), 4)},
+        "clock": clock.report(),
+        "parity": parity,
     }
 
 
@@ -383,25 +488,25 @@ def main():
         o, lse = ext.fa_fwd(q, k, v, 0.0, True, scale, 0)
         ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, scale, 0, args.bwd_mode)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+
+    # The parity check leaves the GPU idle while the host compares results, and
+    # the first ~100 ms of work after such a pause run several percent slow:
+    # untimed steps for 150 ms first, so that every timed figure below sees the
+    # sustained state.
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    while time.perf_counter() - t0 < 0.15:
         step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed / args.steps * 1e3
-    value = step_flops * args.steps / elapsed / 1e12
+        torch.cuda.synchronize()
 
     # Per-kernel launch durations: HIP events around each C-ABI launch on the
-    # current stream (the stream the kernels run on), over K further steps.
+    # current stream (the stream the kernels run on), over max(K, 5) steps after
+    # two untimed ones.
     lib = fa2_capi.load()
     o = torch.empty_like(q)
     lse = torch.empty(B, H, S, device=dev)
     dq, dk, dv = (torch.empty(B, H, S, 64, dtype=torch.float16, device=dev) for _ in range(3))
     ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4, device=dev)
-    stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     pf = fa2_capi.fwd_params(q, k, v, o, lse, scale)
     pb = fa2_capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, scale)
@@ -419,11 +524,38 @@ def main():
     torch.cuda.synchronize()
     avg = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev)
            for j, name in enumerate(("fwd", "bwd_dq", "bwd_dkv"))}
+    med = {name: statistics.median(e[j].elapsed_time(e[j + 1]) for e in ev)
+           for j, name in enumerate(("fwd", "bwd_dq", "bwd_dkv"))}
+    del o, lse, dq, dk, dv, ws
+
+    # The headline: W warm-up steps, then K steps through the drop-in ops, each
+    # bracketed by HIP events on the stream; value = flops / median step.  The
+    # host wall clock over the K steps (which adds launch and allocator time
+    # whenever the host falls behind the GPU) is kept as a secondary figure.
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    sev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    clock = ClockSampler(torch)
+    with clock:
+        t0 = time.perf_counter()
+        sev[0].record(stream)
+        for i in range(args.steps):
+            step()
+            sev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    step_ms = [sev[i].elapsed_time(sev[i + 1]) for i in range(args.steps)]
+    ms_per_step = statistics.median(step_ms)
+    value = step_flops / (ms_per_step / 1e3) / 1e12
+    wall_ms = elapsed / args.steps * 1e3
+
     unit = B * H * S * S * 64
     executed = {"fwd": 2 * unit, "bwd_dq": 3 * unit, "bwd_dkv": 4 * unit}
     dom = max(avg, key=avg.get)
     achieved = executed[dom] / (avg[dom] / 1e3) / 1e12
-    kernels = {kname: {"avg_ms": round(avg[kname], 4), "executed_gflop": round(executed[kname] / 1e9, 2),
+    kernels = {kname: {"avg_ms": round(avg[kname], 4), "median_ms": round(med[kname], 4),
+                       "executed_gflop": round(executed[kname] / 1e9, 2),
                        "tflops": round(executed[kname] / (avg[kname] / 1e3) / 1e12, 1)} for kname in avg}
 
     # Cold L2: each step preceded by a 512 MB buffer write (larger than the
@@ -442,6 +574,12 @@ def main():
     cold_ms = statistics.median(cold)
     timing = {"fwd_ms": round(avg["fwd"], 4), "bwd_ms": round(avg["bwd_dq"] + avg["bwd_dkv"], 4),
               "fwd_bwd_ms": round(sum(avg.values()), 4),
+              "kernel_sum_median_ms": round(sum(med.values()), 4),
+              "step_ms": {"median": round(ms_per_step, 4), "min": round(min(step_ms), 4),
+                          "max": round(max(step_ms), 4), "mean": round(statistics.mean(step_ms), 4),
+                          "wall_mean": round(wall_ms, 4),
+                          "sample": f"HIP events around each of the {args.steps} timed steps on the stream; "
+                                    f"wall_mean = host perf_counter over them / K"},
               "cold_l2": {"ms_per_step": round(cold_ms, 4), "tflops": round(step_flops / (cold_ms / 1e3) / 1e12, 1),
                           "flush_mb": 512, "sample": "median of 10 steps, each after a 512 MB device write"}}
     if not args.no_dropout:
@@ -469,6 +607,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(dom)},
         "kernels": kernels,
         "timing": timing,
+        "clock": clock.report(),
         "parity": parity,
     }
     if not args.no_cpu:

@@ -58,6 +58,9 @@ typedef struct fa2_fwd_params {
     uint32_t seed;                  /* dropout hash seed                       */
     int32_t causal;                 /* nonzero: key j visible to query i iff j <= i */
     uint32_t *dropout_mask;         /* optional keep-bit output, see below; NULL = none */
+    size_t dropout_mask_bytes;      /* bytes at dropout_mask: with dropout_p > 0 at least
+                                       fa2_dropout_mask_bytes(B, H, S), else
+                                       FA2_ERR_WORKSPACE (ignored when dropout_mask is NULL) */
 } fa2_fwd_params;
 
 int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
@@ -79,6 +82,14 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
  * T = 2*ceil(S/128); its bit 31 - (16*kb + 8*hh + e) is key
  * 64*t + 32*kb + 16*hh + 8*(e/4) + 4*g + e%4 (kb, hh in 0..1, e in 0..7). */
 size_t fa2_dropout_mask_bytes(int32_t B, int32_t H, int32_t S);
+
+/* The integer form of the reference's keep test, which every kernel uses:
+ * (h >> 8) * 2^-24 >= p in fp32 (exact, since h >> 8 < 2^24) holds iff
+ * (h >> 8) >= fa2_dropout_threshold(p) = ceil(p * 2^24).  A host function (no
+ * GPU needed), exported so that the equivalence can be checked exhaustively.
+ * Replaces the compare of dropout_keep
+ *   (reference @ None: csrc/flash_attn_v100/fa_common.cuh:37). */
+uint32_t fa2_dropout_threshold(float dropout_p);
 
 /* Forward over a key/value sequence of its own length, for inference callers:
  * a prefill chunk of S new queries against a KV cache of s_k rows, or decode
@@ -142,6 +153,8 @@ typedef struct fa2_bwd_params {
                                            split backward (modes 2, 4, 7), while
                                            the fused backward hashes again, with
                                            the same result; NULL = hash           */
+    size_t dropout_mask_bytes;          /* bytes at dropout_mask, checked like the
+                                           forward's                              */
 } fa2_bwd_params;
 
 /* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta and scaled LSE

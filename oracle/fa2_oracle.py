@@ -27,11 +27,16 @@ How each function is pinned (tests/test_oracle.py):
                        to 0 so dQ is invariant to shifting all keys; sum of dV rows =
                        sum of dO rows at p = 0); torch autograd of an explicit-mask
                        dropout attention for p > 0.
-  dropout_keep         restated from the reference's source text: no golden masks
-                       exist in the reference, so bit-exact parity with it is
-                       *parity unpinned*; tests pin the integer arithmetic against an
-                       independent pure-Python evaluation and the keep rate / mask
-                       statistics.
+  dropout_keep         the finaliser against Wellons' published inverse of lowbias32
+                       (round trip on 10^6 words); the four input multipliers
+                       against the published algorithms they come from (xxHash32
+                       via the ``xxhash`` library, MurmurHash3_x86_32 via
+                       scikit-learn); the fp32 threshold compare against the
+                       integer form the kernels use, over all 2^24 values; planted
+                       one-bit mistakes in every constant and shift fail those
+                       checks.  Which index takes which multiplier (and the +1
+                       offsets) is restated from the source text; the reference
+                       holds no golden masks to pin it further.
   rope_fwd / rope_bwd  torch eager fp32 expression (train.py:1904-1918) and its fp32
                        autograd, then .half(): bitwise.
 """
@@ -46,20 +51,48 @@ LN2 = 0.6931471805599453
 # ---------------------------------------------------------------------------
 _M32 = np.uint64(0xFFFFFFFF)
 
+# Finaliser (fa_common.cuh:21-26): Wellons' published "lowbias32"
+# (hash-prospector), x ^= x >> 16; x *= M1; x ^= x >> 15; x *= M2; x ^= x >> 16.
+LOWBIAS32_MUL = (0x7FEB352D, 0x846CA68B)
+LOWBIAS32_SHIFT = (16, 15, 16)
+# Input mixing (fa_common.cuh:32-35): seed, row + 1, col + 1 and bh + 1 times
+# these multipliers, xor-ed.  They are published constants: xxHash32's
+# PRIME32_1 (seed) and PRIME32_4 (bh), MurmurHash3's fmix32 multipliers (row,
+# col); tests/test_oracle.py checks each against those algorithms.
+DROP_SEED_MUL = 0x9E3779B1
+DROP_ROW_MUL = 0x85EBCA6B
+DROP_COL_MUL = 0xC2B2AE35
+DROP_BH_MUL = 0x27D4EB2F
+
 
 def _u32(x):
     return (np.asarray(x, dtype=np.uint64) & _M32)
 
 
-def hash_u32(x):
-    """lowbias32 finaliser (fa_common.cuh:21-26), vectorised over uint64 holding u32."""
+def hash_u32(x, mul=LOWBIAS32_MUL, shift=LOWBIAS32_SHIFT):
+    """lowbias32 finaliser (fa_common.cuh:21-26), vectorised over uint64 holding u32.
+
+    ``mul``/``shift`` default to the reference's; tests pass altered ones to
+    plant a mistake."""
     x = _u32(x)
-    x = x ^ (x >> np.uint64(16))
-    x = (x * np.uint64(0x7FEB352D)) & _M32
-    x = x ^ (x >> np.uint64(15))
-    x = (x * np.uint64(0x846CA68B)) & _M32
-    x = x ^ (x >> np.uint64(16))
+    x = x ^ (x >> np.uint64(shift[0]))
+    x = (x * np.uint64(mul[0])) & _M32
+    x = x ^ (x >> np.uint64(shift[1]))
+    x = (x * np.uint64(mul[1])) & _M32
+    x = x ^ (x >> np.uint64(shift[2]))
     return x
+
+
+def dropout_hash(seed, row, col, bh, muls=None):
+    """The 32-bit hash of (seed, query row, key col, b*H+h) (fa_common.cuh:30-36).
+
+    ``muls`` = (seed, row, col, bh) multipliers, the reference's by default."""
+    ms, mr, mc, mb = muls or (DROP_SEED_MUL, DROP_ROW_MUL, DROP_COL_MUL, DROP_BH_MUL)
+    h = (_u32(seed) * np.uint64(ms)) & _M32
+    h = h ^ ((_u32(np.asarray(row, np.int64) + 1) * np.uint64(mr)) & _M32)
+    h = h ^ ((_u32(np.asarray(col, np.int64) + 1) * np.uint64(mc)) & _M32)
+    h = h ^ ((_u32(np.asarray(bh, np.int64) + 1) * np.uint64(mb)) & _M32)
+    return hash_u32(h)
 
 
 def dropout_keep(seed, row, col, bh, p):
@@ -67,11 +100,7 @@ def dropout_keep(seed, row, col, bh, p):
 
     ``row``/``col``/``bh`` broadcast.  keep iff (h >> 8) * 2^-24 >= p with the
     compare done in fp32 as the reference does."""
-    h = (_u32(seed) * np.uint64(0x9E3779B1)) & _M32
-    h = h ^ ((_u32(np.asarray(row, np.int64) + 1) * np.uint64(0x85EBCA6B)) & _M32)
-    h = h ^ ((_u32(np.asarray(col, np.int64) + 1) * np.uint64(0xC2B2AE35)) & _M32)
-    h = h ^ ((_u32(np.asarray(bh, np.int64) + 1) * np.uint64(0x27D4EB2F)) & _M32)
-    h = hash_u32(h)
+    h = dropout_hash(seed, row, col, bh)
     u = (h >> np.uint64(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
     return u >= np.float32(p)
 

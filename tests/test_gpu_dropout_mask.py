@@ -115,6 +115,36 @@ def test_autograd_mask_on_off_identical(fa, monkeypatch):
         assert torch.equal(a, b)
 
 
+def test_words_only_when_a_gradient_follows(fa, monkeypatch):
+    """Without a gradient to compute (no_grad, or no input requiring one) the forward stores
+    no keep-bit words; with one, the words are saved for the backward."""
+    say("case words only with a backward")
+    q, k, v, _ = rand_inputs(1, 2, 256, seed=21)
+    ext = fa.extension()
+    calls = []
+
+    class Spy:
+        def __getattr__(self, name):
+            fn = getattr(ext, name)
+            if name == "fa_fwd_mask":
+                def wrapped(*a, **kw):
+                    calls.append(name)
+                    return fn(*a, **kw)
+                return wrapped
+            return fn
+
+    monkeypatch.setattr(fa, "_EXT", Spy())
+    with torch.no_grad():
+        fa.flash_attn_v100(q, k, v, dropout_p=0.2, causal=True)
+    fa.flash_attn_v100(q, k, v, dropout_p=0.2, causal=True)        # no input requires grad
+    assert calls == []
+    qg = q.clone().requires_grad_(True)
+    o = fa.flash_attn_v100(qg, k, v, dropout_p=0.2, causal=True)
+    assert calls == ["fa_fwd_mask"] and o.grad_fn.saved_tensors[5] is not None
+    o.sum().backward()
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("shape", ["config2", "long"])
 def test_full_size_mask_path_bitwise_equals_hash_path(fa, shape):
     """At the benchmark shape (B=8 H=12 S=4096, 201 MB of words) and at S=16384 (B=1 H=2): the word
@@ -135,3 +165,60 @@ def test_full_size_mask_path_bitwise_equals_hash_path(fa, shape):
     torch.cuda.synchronize()
     for name, a, b in zip(("dQ", "dK", "dV"), got, ref):
         assert torch.equal(a, b), f"{name} differs"
+
+
+@pytest.mark.parametrize("use_mask", [False, True])
+def test_config2_dropout_bands_vs_oracle(fa, use_mask):
+    """Config 2 at full size (B=8 H=12 S=4096, RoPE inputs) with p = 0.1, through the
+    hash path and through the keep-bit words: O, LSE, dQ of two 256-row query bands, and
+    dK, dV of the last 256 keys (seen only by the last 256 queries), against fp32
+    computations from the band's [H, 256, S] score slab with the oracle's keep mask for
+    those rows -- P_d = keep * P / (1-p) with LSE from the un-dropped P, dS = P_d * dP - P * delta
+    (reference @ None: flash_attn_v100.cu:208-231, flash_attn_v100_bwd.cu:149-191,373-396).
+    Bars: O max-abs 2e-3 / (1-p), LSE max-abs 1e-3, gradients relative L2 1e-2."""
+    import fa2_workloads as wl
+    say(f"case config-2 dropout bands vs oracle, keep-bit words={use_mask}")
+    ext = fa.extension()
+    q, k, v, do = wl.config_inputs(2, device=DEV)
+    B, H, S, _ = q.shape
+    p, seed, R, scale = 0.1, 0x5EED5, 256, 0.125
+    if use_mask:
+        o, lse, mask = ext.fa_fwd_mask(q, k, v, p, True, scale, seed)
+        dq, dk, dv = ext.fa_bwd(q, k, v, o, lse, do, p, True, scale, seed, 7, mask=mask)
+    else:
+        o, lse = ext.fa_fwd(q, k, v, p, True, scale, seed)
+        dq, dk, dv = ext.fa_bwd(q, k, v, o, lse, do, p, True, scale, seed, 7)
+    torch.cuda.synchronize()
+    rel = lambda a, b: ((a.float() - b).norm() / b.norm()).item()
+    cols = torch.arange(S, device=DEV)
+    for b in (0, B - 1):
+        kf, vf = k[b].float(), v[b].float()                                  # [H, S, 64]
+        for r0 in (S // 2 - R // 2, S - R):
+            rows = np.arange(r0, r0 + R)
+            keep = orc.dropout_keep(seed, rows[None, :, None], np.arange(S)[None, None, :],
+                                    (b * H + np.arange(H))[:, None, None], p)   # [H, R, S]
+            keep = torch.from_numpy(keep).to(DEV).float()
+            s = torch.matmul(q[b, :, r0:r0 + R].float(), kf.transpose(-1, -2).contiguous()) * scale
+            s.masked_fill_(cols.view(1, -1) > torch.arange(r0, r0 + R, device=DEV).view(-1, 1), float("-inf"))
+            rl = torch.logsumexp(s, dim=-1)
+            pr = torch.exp(s - rl.unsqueeze(-1))
+            pd = pr * keep / (1 - p)
+            ro = torch.matmul(pd, vf)
+            dob = do[b, :, r0:r0 + R].float()
+            delta = (ro * dob).sum(-1, keepdim=True)
+            dpm = torch.matmul(dob, vf.transpose(-1, -2).contiguous())
+            ds = pd * dpm - pr * delta
+            rdq = torch.matmul(ds, kf) * scale
+            eo = (o[b, :, r0:r0 + R].float() - ro).abs().max().item()
+            el = (lse[b, :, r0:r0 + R] - rl).abs().max().item()
+            eq = rel(dq[b, :, r0:r0 + R], rdq)
+            say(f"b={b} rows {r0}..{r0 + R - 1}: O maxabs {eo:.2e}  LSE maxabs {el:.2e}  dQ rel {eq:.2e}  "
+                f"kept {keep[:, :, :r0 + 1].mean().item():.4f}")
+            assert eo <= 2e-3 / (1 - p) and el <= 1e-3 and eq <= 1e-2
+            if r0 == S - R:
+                qb = q[b, :, r0:].float()
+                rdv = torch.matmul(pd[:, :, r0:].transpose(-1, -2).contiguous(), dob)
+                rdk = torch.matmul(ds[:, :, r0:].transpose(-1, -2).contiguous(), qb) * scale
+                edv, edk = rel(dv[b, :, r0:], rdv), rel(dk[b, :, r0:], rdk)
+                say(f"b={b} last {R} keys: dK rel {edk:.2e}  dV rel {edv:.2e}")
+                assert edk <= 1e-2 and edv <= 1e-2

@@ -34,6 +34,49 @@ def test_decoder_step_matches_sdpa_path(fa):
         assert e < 1e-2, (n, e)
 
 
+def test_config5_decoder_step_matches_sdpa_fp32(fa):
+    """Benchmark configuration 5 at its full workload: 10 layers, d_model 768, 12 heads,
+    SwiGLU 2048, vocab 32000, B=4, S=4096, fp16 autocast with GradScaler; one training step
+    through flash_attn_v100 / rope against the same weights with attention by SDPA's math
+    backend in fp32 and eager RoPE.  Loss within 1e-3 relative, every parameter gradient
+    within 1e-2 relative."""
+    print("case config-5 decoder step: 10 layers, B=4 S=4096 d_model=768 d_ff=2048 vocab=32000", flush=True)
+    lk, lr, errs = dec.compare_training_step(fa, B=4, S=4096)
+    worst = max(errs, key=errs.get)
+    print(f"loss kernel {lk:.6f} reference {lr:.6f}; worst gradient {worst} rel {errs[worst]:.2e}", flush=True)
+    torch.cuda.empty_cache()
+    assert abs(lk - lr) < 1e-3 * abs(lr)
+    assert errs[worst] < 1e-2, (worst, errs[worst])
+
+
+def test_config1_on_gpu(fa):
+    """Benchmark configuration 1 (B=2 H=4 S=256 D=64, N(0,1), [B,S,H,D] layout) on the GPU:
+    fp32 inputs are not eligible, so flash_attn_v100's caller falls back to SDPA and the
+    module's sdpa() equals F.scaled_dot_product_attention bit for bit; cast to fp16 (train.py's
+    autocast half-cast, train.py:103-113) the kernel matches the fp64 oracle."""
+    import numpy as np
+    import fa2_workloads as wl
+    from oracle import fa2_oracle as orc
+    print("case config 1 on the GPU: B=2 H=4 S=256", flush=True)
+    q, k, v, do = wl.config_inputs(1, device="cuda")
+    assert q.dtype == torch.float32 and not fa.can_use(q, k, v)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+    assert torch.equal(fa.sdpa(q, k, v, is_causal=True), ref)
+    qh, kh, vh, doh = (t.half() for t in (q, k, v, do))
+    assert fa.can_use(qh, kh, vh)
+    qh, kh, vh = (t.detach().requires_grad_(True) for t in (qh, kh, vh))
+    o = fa.flash_attn_v100(qh, kh, vh, causal=True)
+    o.backward(doh)
+    n = lambda t: t.detach().double().cpu().numpy()
+    ro, rlse = orc.attention_dense_fwd(n(qh), n(kh), n(vh), causal=True, scale=0.125)
+    rdq, rdk, rdv = orc.attention_bwd(n(qh), n(kh), n(vh), ro, rlse, n(doh), causal=True, scale=0.125)[:3]
+    eo = np.abs(n(o) - ro).max()
+    rel = lambda a, b: np.linalg.norm(a - b) / np.linalg.norm(b)
+    eg = [rel(n(t.grad), r) for t, r in ((qh, rdq), (kh, rdk), (vh, rdv))]
+    print(f"config 1 fp16 kernel: O maxabs {eo:.2e}  dQ/dK/dV rel {eg[0]:.2e} {eg[1]:.2e} {eg[2]:.2e}", flush=True)
+    assert eo <= 2e-3 and max(eg) <= 1e-2
+
+
 def test_train_layout_output_needs_no_copy(fa):
     """For q/k/v in train.py's (B,S,H,D) memory order the output is stored in
     that order, so attn.transpose(1,2) is already contiguous, and the values

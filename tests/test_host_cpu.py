@@ -9,6 +9,7 @@ import os
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -140,6 +141,36 @@ def test_dropout_mask_size_and_validation():
     need = lib.fa2_bwd_workspace_bytes(1, 1, 64)
     assert lib.fa2_bwd_f16(ctypes.byref(pb), 7, ctypes.c_void_p(1 << 22), need, None) == 3
     assert b"dropout_mask" in lib.fa2_last_error()
+    # An undersized mask buffer (the device writes would run past it) is rejected before any
+    # launch, in the forward and the backward; its size only matters when dropout uses it.
+    fwd_need = lib.fa2_dropout_mask_bytes(2, 8, 16)
+    p = _dummy_fwd(dropout_p=0.1, dropout_mask=1 << 21, dropout_mask_bytes=fwd_need - 4)
+    assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 5, lib.fa2_last_error()
+    assert b"dropout_mask needs" in lib.fa2_last_error()
+    pb.dropout_mask, pb.dropout_mask_bytes = base, lib.fa2_dropout_mask_bytes(1, 1, 64) - 16
+    assert lib.fa2_bwd_f16(ctypes.byref(pb), 7, ctypes.c_void_p(1 << 22), need, None) == 5
+    assert b"dropout_mask needs" in lib.fa2_last_error()
+    pb.dropout_p = 0.0     # no dropout: the mask is not used, so its size is not checked
+    assert lib.fa2_bwd_f16(ctypes.byref(pb), 0, ctypes.c_void_p(1 << 22), need, None) == 0
+
+
+# p values: the tests' own, values whose p * 2^24 is not an integer, values next to a
+# multiple of 2^-24, and the extremes of [0, 1).
+THRESHOLD_PS = [0.1, 0.25, 0.5, 0.9, 1 / 3, 0.123456789, 0.7, 5e-8, 2.0 ** -24, 3 * 2.0 ** -24,
+                float(np.nextafter(np.float32(0.5), np.float32(1))),
+                float(np.nextafter(np.float32(0.5), np.float32(0))), 0.0, 0.99999994]
+
+
+@pytest.mark.parametrize("p", THRESHOLD_PS)
+def test_dropout_threshold_equals_reference_fp32_compare_exhaustively(p):
+    """Every kernel keeps an element iff (h >> 8) >= fa2_dropout_threshold(p); the reference
+    keeps it iff (h >> 8) * 2^-24 >= p in fp32 (fa_common.cuh:37).  Both over all 2^24
+    values of h >> 8."""
+    lib = capi.load()
+    thr = lib.fa2_dropout_threshold(p)
+    v = np.arange(1 << 24, dtype=np.uint32)
+    ref = v.astype(np.float32) * np.float32(1.0 / 16777216.0) >= np.float32(p)
+    assert np.array_equal(ref, v >= thr), (p, thr)
 
 
 def test_bwd_validation():

@@ -162,28 +162,147 @@ def test_bwd_invariants_and_planted_mistakes():
     assert not _invariants_hold(wrong_lse, q, k, v, do)
 
 
-def _keep_py(seed, row, col, bh, p):
-    """Pure-Python integer evaluation of the reference's dropout hash."""
-    M = 0xFFFFFFFF
-    h = (seed * 0x9E3779B1) & M
-    h ^= ((row + 1) * 0x85EBCA6B) & M
-    h ^= ((col + 1) * 0xC2B2AE35) & M
-    h ^= ((bh + 1) * 0x27D4EB2F) & M
-    h ^= h >> 16
-    h = (h * 0x7FEB352D) & M
+# --- dropout hash: each part against the published function it comes from ----------
+_M = 0xFFFFFFFF
+
+
+def _lowbias32_inverse(x):
+    """Wellons' published inverse of lowbias32 (hash-prospector), uint64 arrays holding u32."""
+    x = x ^ (x >> 16)
+    x = (x * 0x43021123) & _M
+    x = x ^ (x >> 15) ^ (x >> 30)
+    x = (x * 0x1D69E2A5) & _M
+    return x ^ (x >> 16)
+
+
+def _round_trips(**planted):
+    x = np.random.default_rng(11).integers(0, 2 ** 32, size=1_000_000, dtype=np.uint64)
+    return np.array_equal(_lowbias32_inverse(orc.hash_u32(x, **planted)), x)
+
+
+def test_dropout_finaliser_is_published_lowbias32():
+    """The oracle's finaliser inverts through the published inverse on 10^6 random words."""
+    assert _round_trips()
+
+
+@pytest.mark.parametrize("which,bit", [(0, 0), (0, 13), (0, 30), (1, 1), (1, 22), (1, 31)])
+def test_dropout_finaliser_planted_multiplier_bit(which, bit):
+    mul = list(orc.LOWBIAS32_MUL)
+    mul[which] ^= 1 << bit
+    assert not _round_trips(mul=tuple(mul))
+
+
+@pytest.mark.parametrize("which,delta", [(0, 1), (1, -1), (1, 1), (2, -1)])
+def test_dropout_finaliser_planted_shift(which, delta):
+    shift = list(orc.LOWBIAS32_SHIFT)
+    shift[which] += delta
+    assert not _round_trips(shift=tuple(shift))
+
+
+def _rotl(x, r):
+    return ((x << r) | (x >> (32 - r))) & _M
+
+
+def _xxh32(data, seed, p1, p4):
+    """XXH32 (Collet's published algorithm) with PRIME32_1 = p1 and PRIME32_4 = p4."""
+    p2, p3, p5 = 0x85EBCA77, 0xC2B2AE3D, 0x165667B1
+    n, i = len(data), 0
+    word = lambda j: int.from_bytes(data[j:j + 4], "little")
+    if n >= 16:
+        v = [(seed + p1 + p2) & _M, (seed + p2) & _M, seed, (seed - p1) & _M]
+        while i + 16 <= n:
+            for lane in range(4):
+                v[lane] = (_rotl((v[lane] + word(i + 4 * lane) * p2) & _M, 13) * p1) & _M
+            i += 16
+        h = (_rotl(v[0], 1) + _rotl(v[1], 7) + _rotl(v[2], 12) + _rotl(v[3], 18)) & _M
+    else:
+        h = (seed + p5) & _M
+    h = (h + n) & _M
+    while i + 4 <= n:
+        h = (_rotl((h + word(i) * p3) & _M, 17) * p4) & _M
+        i += 4
+    while i < n:
+        h = (_rotl((h + data[i] * p5) & _M, 11) * p1) & _M
+        i += 1
     h ^= h >> 15
-    h = (h * 0x846CA68B) & M
+    h = (h * p2) & _M
+    h ^= h >> 13
+    h = (h * p3) & _M
+    return h ^ (h >> 16)
+
+
+def _murmur3_x86_32_u32(key, seed, f1, f2):
+    """MurmurHash3_x86_32 (Appleby's published algorithm) of a 4-byte key with the
+    fmix32 multipliers f1, f2."""
+    k = (key * 0xCC9E2D51) & _M
+    k = (_rotl(k, 15) * 0x1B873593) & _M
+    h = _rotl(seed ^ k, 13)
+    h = (h * 5 + 0xE6546B64) & _M
+    h ^= 4
     h ^= h >> 16
-    return (h >> 8) >= math.ceil(float(np.float32(p)) * 16777216.0)
+    h = (h * f1) & _M
+    h ^= h >> 13
+    h = (h * f2) & _M
+    return h ^ (h >> 16)
 
 
-def test_dropout_hash_integer_arithmetic():
-    rng = np.random.default_rng(5)
-    for _ in range(300):
+def _xxh32_matches(p1, p4):
+    import xxhash
+    rng = np.random.default_rng(12)
+    for n in list(range(0, 41)) + [64, 100]:
+        data = rng.integers(0, 256, size=n, dtype=np.uint8).tobytes()
         seed = int(rng.integers(0, 2 ** 32))
-        row, col, bh = (int(x) for x in rng.integers(0, 70000, size=3))
-        p = float(rng.choice([0.0, 0.1, 0.25, 0.5, 0.9]))
-        assert bool(orc.dropout_keep(seed, row, col, bh, p)) == _keep_py(seed, row, col, bh, p)
+        if _xxh32(data, seed, p1, p4) != xxhash.xxh32_intdigest(data, seed):
+            return False
+    return True
+
+
+def _murmur3_matches(f1, f2):
+    from sklearn.utils import murmurhash3_32
+    rng = np.random.default_rng(13)
+    for _ in range(200):
+        key, seed = int(rng.integers(-2 ** 31, 2 ** 31)), int(rng.integers(0, 2 ** 31))
+        want = murmurhash3_32(key, seed=seed, positive=True)
+        if _murmur3_x86_32_u32(key & _M, seed, f1, f2) != want:
+            return False
+    return True
+
+
+def test_dropout_mixing_multipliers_are_published_constants():
+    """The seed and bh multipliers are xxHash32's PRIME32_1 and PRIME32_4 (checked against
+    the xxhash library), the row and col multipliers MurmurHash3's fmix32 pair (checked
+    against scikit-learn's MurmurHash3_x86_32)."""
+    assert _xxh32_matches(orc.DROP_SEED_MUL, orc.DROP_BH_MUL)
+    assert _murmur3_matches(orc.DROP_ROW_MUL, orc.DROP_COL_MUL)
+    # odd multipliers: each term is a bijection of its index modulo 2^32
+    for m in (orc.DROP_SEED_MUL, orc.DROP_ROW_MUL, orc.DROP_COL_MUL, orc.DROP_BH_MUL):
+        assert m & 1
+
+
+@pytest.mark.parametrize("which", range(4))
+@pytest.mark.parametrize("bit", [0, 7, 19, 31])
+def test_dropout_mixing_planted_bit(which, bit):
+    muls = [orc.DROP_SEED_MUL, orc.DROP_ROW_MUL, orc.DROP_COL_MUL, orc.DROP_BH_MUL]
+    muls[which] ^= 1 << bit
+    ok = _xxh32_matches(muls[0], muls[3]) and _murmur3_matches(muls[1], muls[2])
+    assert not ok
+    # and the oracle's hash built on the altered constant changes
+    rng = np.random.default_rng(14)
+    seed, row, col, bh = (rng.integers(0, 5000, size=64) for _ in range(4))
+    assert not np.array_equal(orc.dropout_hash(seed, row, col, bh, muls=tuple(muls)),
+                              orc.dropout_hash(seed, row, col, bh))
+
+
+def test_dropout_keep_uses_the_fp32_threshold_compare():
+    """keep == ((hash >> 8) * 2^-24 >= p in fp32), element for element."""
+    rng = np.random.default_rng(5)
+    seed = 0xC0FFEE
+    row, col = rng.integers(0, 70000, size=(2, 4096))
+    bh = rng.integers(0, 96, size=4096)
+    h = orc.dropout_hash(seed, row, col, bh)
+    for p in (0.0, 0.1, 0.5, 0.9, 1 / 3):
+        u = (h >> np.uint64(8)).astype(np.float32) * np.float32(2.0 ** -24)
+        assert np.array_equal(orc.dropout_keep(seed, row, col, bh, p), u >= np.float32(p))
 
 
 def test_dropout_statistics():

@@ -68,20 +68,27 @@ float scale2_of(float scale) {
     return s2 < FLT_MIN ? FLT_MIN : s2;
 }
 
-// The keep-bit words are moved in 16-byte transfers; without dropout they
-// are not touched.
-int check_mask(const void *mask, float p) {
-    if (mask && p > 0.f && (reinterpret_cast<uintptr_t>(mask) & 15u))
-        return fail(FA2_ERR_MISALIGNED, "dropout_mask is not 16-byte aligned");
+// The keep-bit words are moved in 16-byte transfers and cover every (b, h)
+// at fixed offsets; without dropout they are not touched.
+int check_mask(const void *mask, size_t bytes, int32_t B, int32_t H, int32_t S, float p) {
+    if (!mask || !(p > 0.f)) return FA2_OK;
+    if (reinterpret_cast<uintptr_t>(mask) & 15u) return fail(FA2_ERR_MISALIGNED, "dropout_mask is not 16-byte aligned");
+    const size_t need = fa2_dropout_mask_bytes(B, H, S);
+    if (bytes < need) return fail(FA2_ERR_WORKSPACE, "dropout_mask needs %zu bytes, got %zu", need, bytes);
     return FA2_OK;
 }
-
-// keep iff (hash >> 8) * 2^-24 >= p  <=>  (hash >> 8) >= ceil(p * 2^24)
-uint32_t drop_threshold(float p) { return (uint32_t)ceilf(p * 16777216.0f); }
 
 }  // namespace
 
 extern "C" {
+
+// keep iff (hash >> 8) * 2^-24 >= p  <=>  (hash >> 8) >= ceil(p * 2^24): p * 2^24
+// is exact in fp32 (a power-of-two scaling) and so is its ceiling.
+uint32_t fa2_dropout_threshold(float p) {
+    if (!(p > 0.f)) return 0;
+    if (!(p < 1.f)) return 1u << 24;
+    return (uint32_t)ceilf(p * 16777216.0f);
+}
 
 const char *fa2_status_string(int status) {
     switch (status) {
@@ -155,7 +162,7 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
     if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
     if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
-    if ((rc = check_mask(p->dropout_mask, p->dropout_p))) return rc;
+    if ((rc = check_mask(p->dropout_mask, p->dropout_mask_bytes, p->B, p->H, p->S, p->dropout_p))) return rc;
 
     fa2::FwdArgs a;
     a.q = static_cast<const _Float16 *>(p->q);
@@ -179,7 +186,7 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     a.scale2 = scale2_of(p->softmax_scale);
     a.negate = p->softmax_scale < 0.f;
     a.seed = p->seed;
-    a.drop_thr = drop_threshold(p->dropout_p);
+    a.drop_thr = fa2_dropout_threshold(p->dropout_p);
     a.inv_keep = 1.f / (1.f - p->dropout_p);
     const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
     a.drop_mask = dropout ? p->dropout_mask : nullptr;
@@ -250,7 +257,7 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
         if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
         if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
         if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
-        if ((rc = check_mask(p->dropout_mask, p->dropout_p))) return rc;
+        if ((rc = check_mask(p->dropout_mask, p->dropout_mask_bytes, p->B, p->H, p->S, p->dropout_p))) return rc;
     }
     struct Out { const char *name; void *ptr; const int64_t *st; };
     const Out outs[3] = {{"dq", p->dq, p->dq_stride}, {"dk", p->dk, p->dk_stride}, {"dv", p->dv, p->dv_stride}};
@@ -293,7 +300,7 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
     a.scale2 = scale2_of(p->softmax_scale);
     a.negate = p->softmax_scale < 0.f;
     a.seed = p->seed;
-    a.drop_thr = drop_threshold(p->dropout_p);
+    a.drop_thr = fa2_dropout_threshold(p->dropout_p);
     a.inv_keep = 1.f / (1.f - p->dropout_p);
     const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
     a.drop_mask = dropout ? p->dropout_mask : nullptr;

@@ -109,6 +109,7 @@ std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor 
         auto mask = torch::empty({dropout_p > 0.0 ? (int64_t)(fa2_dropout_mask_bytes(p.B, p.H, p.S) / 4) : 0},
                                  q.options().dtype(torch::kInt));
         p.dropout_mask = dropout_p > 0.0 ? reinterpret_cast<uint32_t *>(mask.data_ptr()) : nullptr;
+        p.dropout_mask_bytes = (size_t)mask.numel() * 4;
         check_status(fa2_fwd_f16(&p, current_stream(q)), op);
         return {o, lse, mask};
     }
@@ -236,7 +237,10 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     p.dropout_p = (float)dropout_p;
     p.seed = (uint32_t)seed;
     p.causal = causal ? 1 : 0;
-    if (mask && dropout_p > 0.0) p.dropout_mask = reinterpret_cast<const uint32_t *>(mask->data_ptr());
+    if (mask && dropout_p > 0.0) {
+        p.dropout_mask = reinterpret_cast<const uint32_t *>(mask->data_ptr());
+        p.dropout_mask_bytes = (size_t)mask->numel() * 4;
+    }
     // The workspace is fresh each call, so a dK/dV-only request also computes
     // delta (the reference would read an uninitialised buffer there).
     int32_t m = (int32_t)mode;

@@ -25,7 +25,7 @@ class FwdParams(ctypes.Structure):
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("S", ctypes.c_int32), ("D", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint32), ("causal", ctypes.c_int32),
-        ("dropout_mask", ctypes.c_void_p),
+        ("dropout_mask", ctypes.c_void_p), ("dropout_mask_bytes", ctypes.c_size_t),
     ]
 
 
@@ -40,7 +40,7 @@ class BwdParams(ctypes.Structure):
         ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("S", ctypes.c_int32), ("D", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint32), ("causal", ctypes.c_int32),
-        ("dropout_mask", ctypes.c_void_p),
+        ("dropout_mask", ctypes.c_void_p), ("dropout_mask_bytes", ctypes.c_size_t),
     ]
 
 
@@ -83,6 +83,8 @@ def load():
         lib.fa2_fwd_kv_workspace_bytes.restype = ctypes.c_size_t
         lib.fa2_dropout_mask_bytes.argtypes = [ctypes.c_int32] * 3
         lib.fa2_dropout_mask_bytes.restype = ctypes.c_size_t
+        lib.fa2_dropout_threshold.argtypes = [ctypes.c_float]
+        lib.fa2_dropout_threshold.restype = ctypes.c_uint32
         lib.fa2_bwd_f16.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int32, ctypes.c_void_p,
                                     ctypes.c_size_t, ctypes.c_void_p]
         lib.fa2_bwd_f16.restype = ctypes.c_int
@@ -107,6 +109,7 @@ def strides3(t):
 def fwd_params(q, k, v, o, lse, scale, causal=True, dropout_p=0.0, seed=0, mask=None):
     p = FwdParams()
     p.dropout_mask = mask.data_ptr() if mask is not None else None
+    p.dropout_mask_bytes = mask.numel() * mask.element_size() if mask is not None else 0
     p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr()
     p.q_stride, p.k_stride, p.v_stride, p.o_stride = strides3(q), strides3(k), strides3(v), strides3(o)
     p.lse_stride = I64x2(lse.stride(0), lse.stride(1))
@@ -118,6 +121,7 @@ def fwd_params(q, k, v, o, lse, scale, causal=True, dropout_p=0.0, seed=0, mask=
 def bwd_params(q, k, v, o, lse, do, dq, dk, dv, scale, causal=True, dropout_p=0.0, seed=0, mask=None):
     p = BwdParams()
     p.dropout_mask = mask.data_ptr() if mask is not None else None
+    p.dropout_mask_bytes = mask.numel() * mask.element_size() if mask is not None else 0
     p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr()
     p.lse, p.dq, p.dk, p.dv = lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
     p.q_stride, p.k_stride, p.v_stride = strides3(q), strides3(k), strides3(v)

@@ -32,6 +32,9 @@ class Attention(nn.Module):
         self.wo = nn.Linear(d_model, d_model, bias=False)
         self.fa, self.use_kernel = fa, use_kernel
         self.attn_fn = None  # optional override (q, k, v) -> o, used for timing
+        # Fallback path only: attention through SDPA's math backend in fp32 (the
+        # reference path the kernel's parity is defined against), cast back.
+        self.ref_fp32 = False
 
     def forward(self, x, cos, sin):
         B, S, D = x.shape
@@ -49,6 +52,10 @@ class Attention(nn.Module):
             q, k, v = (t.half() if t.dtype == torch.float32 else t for t in (q, k, v))
         if fa is not None and fa.can_use(q, k, v):
             attn = self.attn_fn(q, k, v) if self.attn_fn else fa.flash_attn_v100(q, k, v, causal=True)
+        elif self.ref_fp32:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            with torch.autocast(x.device.type, enabled=False), sdpa_kernel(SDPBackend.MATH):
+                attn = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True).to(q.dtype)
         else:
             attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         return self.wo(attn.transpose(1, 2).contiguous().view(B, S, D))
@@ -142,6 +149,36 @@ class Decoder(nn.Module):
     def loss(self, ids):
         logits = self.forward(ids[:, :-1])
         return F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), ids[:, 1:].reshape(-1))
+
+
+def compare_training_step(fa, B, S, n_layers=10, d_ff=2048, vocab=32000, seed=0, device="cuda"):
+    """One fp16-autocast training step (GradScaler-scaled backward, then unscaled
+    gradients) of the same random-init weights through the kernel path
+    (``flash_attn_v100`` + fused ``rope``) and through the reference path (eager
+    RoPE, attention by SDPA's math backend in fp32), as train.py's loop runs it
+    (reference @ None: train.py:1931-1964, 2341-2424).  Returns (loss_kernel,
+    loss_reference, {parameter name: relative L2 error of its gradient})."""
+    torch.manual_seed(seed)
+    mk = Decoder(vocab=vocab, n_layers=n_layers, d_ff=d_ff, fa=fa, use_kernel=True).to(device)
+    mr = Decoder(vocab=vocab, n_layers=n_layers, d_ff=d_ff, fa=None, use_kernel=False).to(device)
+    mr.load_state_dict(mk.state_dict())
+    for layer in mr.layers:
+        layer.attn.ref_fp32 = True
+    ids = synthetic_ids(B, S, vocab=vocab, seed=seed + 1, device=device)
+    losses = []
+    for m in (mk, mr):
+        opt = torch.optim.SGD(m.parameters(), lr=0.0)
+        scaler = torch.amp.GradScaler(device, init_scale=2.0 ** 16)
+        with torch.autocast(device, dtype=torch.float16):
+            loss = m.loss(ids)
+        scaler.scale(loss).backward()
+        scaler.unscale_(opt)
+        losses.append(loss.item())
+    errs = {}
+    for (n, pk), (_, pr) in zip(mk.named_parameters(), mr.named_parameters()):
+        errs[n] = ((pk.grad.float() - pr.grad.float()).norm() / pr.grad.float().norm()).item()
+    del mk, mr
+    return losses[0], losses[1], errs
 
 
 def synthetic_ids(B, S, vocab=32000, seed=0, device="cpu"):

@@ -53,13 +53,19 @@ _EXT = None
 _BUILD_ERROR = None
 
 # The backward must reuse the forward's dropout mask.  The mask is a pure
-# function of (seed, row, col, bh), so saving the seed in ctx is enough.
+# function of (seed, row, col, bh), so the seed alone (saved in ctx) lets the
+# backward hash it again.
 _SEED_COUNTER = itertools.count(1)
 
-# With dropout the forward also stores its keep bits (one bit per query/key
-# pair, held until the backward), which the backward then reads instead of
-# hashing again: identical gradients, less backward work.  A call whose words
-# would exceed this many bytes hashes in the backward instead.
+# Keep-bit words: with dropout, and only when a gradient of q, k or v will be
+# computed, the forward also stores its keep bits (one bit per query/key pair
+# of the square, 201 MB at B=8 H=12 S=4096), saved with the other tensors until
+# the backward, which then reads them instead of hashing again: identical
+# gradients, less backward work.  The words live as long as the autograd graph
+# holds them, i.e. one set per attention call awaiting its backward (ten for a
+# ten-layer model).  This cap applies to each call's words on their own, not to
+# their total: a call whose words would exceed it hashes in the backward
+# instead (seed only), and a cap of 0 turns the words off.
 def _mask_cap(default=1 << 30):
     text = os.environ.get("FA_V100_DROPOUT_MASK_MAX_BYTES", "")
     try:
@@ -132,7 +138,8 @@ class _FlashAttnV100Cuda(torch.autograd.Function):
         ext = extension()
         seed = _next_seed()
         mask = None
-        if dropout_p > 0 and dropout_mask_bytes(*q.shape[:3]) <= DROPOUT_MASK_MAX_BYTES:
+        if (dropout_p > 0 and any(ctx.needs_input_grad[:3])
+                and dropout_mask_bytes(*q.shape[:3]) <= DROPOUT_MASK_MAX_BYTES):
             o, lse, mask = ext.fa_fwd_mask(q, k, v, float(dropout_p), bool(causal), float(softmax_scale), int(seed))
         else:
             o, lse = ext.fa_fwd(q, k, v, float(dropout_p), bool(causal), float(softmax_scale), int(seed))
