@@ -166,6 +166,29 @@ size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S);
 int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,
                 size_t workspace_bytes, void *stream);
 
+/* Allocation-free backward: fa2_bwd_f16 (modes 0..7, same kernels, same
+ * results bit for bit) with no workspace argument.  Its workspace is scratch
+ * memory inside the library: a device array of FA2_BWD_SCRATCH_MAX_BYTES that
+ * every GPU the library runs on holds from the first use until the process
+ * ends.  The call allocates nothing and frees nothing, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); the caller still provides inputs and outputs.
+ *   - Size limit: fa2_bwd_noalloc_scratch_bytes(B, H, S) (delta, scaled LSE and
+ *     the row terms: about 24*B*H*S bytes) must not exceed
+ *     FA2_BWD_SCRATCH_MAX_BYTES, else FA2_ERR_WORKSPACE; the fused backward
+ *     (mode bit 8, which needs a 256*B*H*S-byte accumulator) is rejected with
+ *     FA2_ERR_BAD_ARGUMENT.
+ *   - Sharing: all calls on one GPU share that GPU's array, which keeps the last
+ *     call's contents.  Calls that overlap in time on one GPU (several streams
+ *     or host threads) race on it and must be serialised by the caller.  Mode 4
+ *     reads the delta an earlier mode 1 or 2 call left there, so that pair must
+ *     run back to back on one stream with no other call in between.
+ * No counterpart in the reference: its fa_bwd allocates its delta buffer and
+ * outputs per call (reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:461-464). */
+#define FA2_BWD_SCRATCH_MAX_BYTES (32u << 20)
+size_t fa2_bwd_noalloc_scratch_bytes(int32_t B, int32_t H, int32_t S);
+int fa2_bwd_f16_noalloc(const fa2_bwd_params *p, int32_t mode, void *stream);
+
 /* Fused rotary embedding on q and k (head_dim 64), fp32 arithmetic with one
  * fp16 rounding, no fused multiply-add (bitwise equal to the eager fp32 path
  * followed by .half()):

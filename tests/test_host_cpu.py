@@ -173,6 +173,23 @@ def test_dropout_threshold_equals_reference_fp32_compare_exhaustively(p):
     assert np.array_equal(ref, v >= thr), (p, thr)
 
 
+def test_bwd_noalloc_rejects_before_any_hip_call():
+    """The allocation-free backward checks its size limit and mode before touching the
+    device (it would otherwise look up its scratch array on the current GPU)."""
+    lib = capi.load()
+    assert lib.fa2_bwd_noalloc_scratch_bytes(2, 3, 5) == 256 + 2 * 3 * 32 * 16
+    assert lib.fa2_bwd_noalloc_scratch_bytes(0, 3, 5) == 0
+    p = capi.BwdParams()
+    p.B, p.H, p.S, p.D, p.softmax_scale = 64, 64, 4096, 64, 0.125
+    assert lib.fa2_bwd_f16_noalloc(ctypes.byref(p), 7, None) == 5
+    assert b"FA2_BWD_SCRATCH_MAX_BYTES" in lib.fa2_last_error()
+    p.S = 64
+    assert lib.fa2_bwd_f16_noalloc(ctypes.byref(p), 14, None) == 4   # fused: needs an accumulator
+    assert lib.fa2_bwd_f16_noalloc(ctypes.byref(p), 16, None) == 4   # bad mode
+    assert lib.fa2_bwd_f16_noalloc(ctypes.byref(p), 0, None) == 0    # nothing requested
+    assert lib.fa2_bwd_f16_noalloc(None, 7, None) == 1
+
+
 def test_bwd_validation():
     lib = capi.load()
     p = capi.BwdParams()

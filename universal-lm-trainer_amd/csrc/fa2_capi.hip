@@ -7,6 +7,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/fa2_mi355x.h"
 #include "fa2_kernels.h"
 
@@ -230,22 +232,25 @@ size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S) {
     return delta_bytes(B, H, S) + terms_bytes(B, H, S) + (size_t)B * H * S * FA2_HEAD_DIM * sizeof(float);
 }
 
-int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t workspace_bytes, void *stream) {
-    g_err[0] = 0;
+// Checks of fa2_bwd_f16 that come before its workspace: status, or -1 when
+// the call has nothing to do (empty problem or mode 0) and returns FA2_OK.
+static int bwd_precheck(const fa2_bwd_params *p, int32_t mode) {
     if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
     if (mode < 0 || mode > 15) return fail(FA2_ERR_BAD_ARGUMENT, "mode %d outside 0..15", mode);
     int rc = check_shape(p->B, p->H, p->S, p->D, 256);
     if (rc) return rc;
     if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
-    if ((int64_t)p->B * p->H * p->S == 0 || mode == 0) return FA2_OK;
+    if ((int64_t)p->B * p->H * p->S == 0 || mode == 0) return -1;
     // The dK/dV pass reaches the LSE copy with a 32-bit byte offset from delta.
     if ((int64_t)p->B * p->H * p->S >= (int64_t)1 << 30)
         return fail(FA2_ERR_BAD_SHAPE, "B*H*S = %lld is not below 2^30", (long long)p->B * p->H * p->S);
-    const size_t need = fa2_bwd_workspace_bytes(p->B, p->H, p->S);
-    if (!workspace || workspace_bytes < need)
-        return fail(FA2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : 0);
-    if (reinterpret_cast<uintptr_t>(workspace) & 15u)
-        return fail(FA2_ERR_MISALIGNED, "workspace is not 16-byte aligned");
+    return FA2_OK;
+}
+
+// The backward on a workspace already checked to hold what `mode` uses:
+// delta, scaled LSE and row terms, plus the dQ accumulator when fused.
+static int bwd_run(const fa2_bwd_params *p, int32_t mode, void *workspace, void *stream) {
+    int rc;
     const bool want_delta = mode & 1, want_dq = mode & 2, want_dkv = mode & 4;
     const bool fused = want_dq && want_dkv && (mode & 8);
     if ((rc = check_tensor("o", p->o, p->o_stride, p->B, p->H, p->S, true))) return rc;
@@ -329,6 +334,79 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t w
         if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "dK/dV launch: %s", hipGetErrorString(e));
     }
     return FA2_OK;
+}
+
+int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    int rc = bwd_precheck(p, mode);
+    if (rc) return rc < 0 ? FA2_OK : rc;
+    const size_t need = fa2_bwd_workspace_bytes(p->B, p->H, p->S);
+    if (!workspace || workspace_bytes < need)
+        return fail(FA2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace ? workspace_bytes : 0);
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u)
+        return fail(FA2_ERR_MISALIGNED, "workspace is not 16-byte aligned");
+    return bwd_run(p, mode, workspace, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free backward: the workspace is `scratch`, a device array of
+// FA2_BWD_SCRATCH_MAX_BYTES that every GPU the library runs on holds from the
+// module's load until the process ends.  In host code `scratch` names a
+// host-side stand-in, never the device memory: the device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only
+// that address is passed on.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[FA2_BWD_SCRATCH_MAX_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's copy of `scratch` (set up on the
+// first call on that device), or a status.
+int scratch_for_current_device(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(FA2_ERR_LAUNCH, "device ordinal %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(FA2_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return FA2_OK;
+}
+}  // namespace
+
+extern "C" {
+
+size_t fa2_bwd_noalloc_scratch_bytes(int32_t B, int32_t H, int32_t S) {
+    if (B <= 0 || H <= 0 || S <= 0) return 0;
+    return delta_bytes(B, H, S) + terms_bytes(B, H, S);
+}
+
+int fa2_bwd_f16_noalloc(const fa2_bwd_params *p, int32_t mode, void *stream) {
+    g_err[0] = 0;
+    int rc = bwd_precheck(p, mode);
+    if (rc) return rc < 0 ? FA2_OK : rc;
+    if ((mode & 14) == 14)
+        return fail(FA2_ERR_BAD_ARGUMENT, "mode %d: the fused backward (bit 8) needs an fp32 dQ accumulator; "
+                    "fa2_bwd_f16_noalloc runs the split backward only", mode);
+    const size_t need = fa2_bwd_noalloc_scratch_bytes(p->B, p->H, p->S);
+    if (need > (size_t)FA2_BWD_SCRATCH_MAX_BYTES)
+        return fail(FA2_ERR_WORKSPACE, "B=%d H=%d S=%d needs %zu bytes of scratch; fa2_bwd_f16_noalloc holds "
+                    "%zu (FA2_BWD_SCRATCH_MAX_BYTES): use fa2_bwd_f16 with a workspace",
+                    p->B, p->H, p->S, need, (size_t)FA2_BWD_SCRATCH_MAX_BYTES);
+    void *ws = nullptr;
+    if ((rc = scratch_for_current_device(&ws))) return rc;
+    return bwd_run(p, mode, ws, stream);
 }
 
 int fa2_rope_f16(const fa2_rope_params *p, int32_t backward, void *stream) {

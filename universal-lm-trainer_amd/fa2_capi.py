@@ -90,6 +90,10 @@ def load():
         lib.fa2_bwd_f16.restype = ctypes.c_int
         lib.fa2_bwd_workspace_bytes.argtypes = [ctypes.c_int32] * 3
         lib.fa2_bwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.fa2_bwd_f16_noalloc.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int32, ctypes.c_void_p]
+        lib.fa2_bwd_f16_noalloc.restype = ctypes.c_int
+        lib.fa2_bwd_noalloc_scratch_bytes.argtypes = [ctypes.c_int32] * 3
+        lib.fa2_bwd_noalloc_scratch_bytes.restype = ctypes.c_size_t
         lib.fa2_rope_f16.argtypes = [ctypes.POINTER(RopeParams), ctypes.c_int32, ctypes.c_void_p]
         lib.fa2_rope_f16.restype = ctypes.c_int
         lib.fa2_status_string.argtypes = [ctypes.c_int]
