@@ -5,7 +5,10 @@ Produces, next to this file under ``lib/``:
     ``include/fa2_mi355x.h`` (hipcc, --offload-arch=gfx950);
   * ``_fa2_torch<EXT_SUFFIX>`` -- the thin PyTorch-ROCm extension exposing the
     reference's ``fa_fwd``/``fa_bwd``/``rope_fwd``/``rope_bwd`` ops on top of
-    that C ABI (g++, linked with an ``$ORIGIN`` rpath).
+    that C ABI (g++, linked with an ``$ORIGIN`` rpath);
+  * ``probe_dq_atomics`` -- a stand-alone measurement of the fp32-atomic dQ
+    accumulation traffic a fused backward would issue (the evidence behind
+    the split dQ pass), run under rocprofv3.
 
 Run ``python universal-lm-trainer_amd/build.py`` (or ``__graft_entry__.build()``).
 No GPU is needed: hipcc cross-compiles for gfx950.
@@ -103,10 +106,24 @@ def build_extension(verbose=False):
     return ext_path()
 
 
+def probe_path():
+    return os.path.join(LIB, "probe_dq_atomics")
+
+
+def build_probe(verbose=False):
+    tmp = probe_path() + ".tmp"
+    out = _run([HIPCC, *[f for f in HIP_FLAGS if f != "-fPIC"], os.path.join(CSRC, "probe_dq_atomics.hip"), "-o", tmp])
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, probe_path())
+    return probe_path()
+
+
 def build(verbose=False):
     build_library(verbose)
     build_extension(verbose)
-    return lib_path(), ext_path()
+    build_probe(verbose)
+    return lib_path(), ext_path(), probe_path()
 
 
 if __name__ == "__main__":
