@@ -234,6 +234,36 @@ def cpu_baseline():
     }
 
 
+def rope_timing(torch, ext, B, H, S, stream, n=20):
+    """Fused RoPE (rope_fwd / rope_bwd) at the configuration's shape on q, k
+    views of a fused qkv tensor, as train.py hands them over
+    (reference @ None: train.py:1909-1913): mean of n calls between HIP events,
+    and the rate of its compulsory HBM bytes (q, k read and written, cos and
+    sin rows read) against 8 TB/s."""
+    import fa2_workloads as wl
+    qkv = torch.randn(B, S, 3 * H * 64, device="cuda", dtype=torch.float16)
+    q, k, _ = (t.view(B, S, H, 64).transpose(1, 2) for t in qkv.chunk(3, dim=-1))
+    cos, sin = (t.cuda() for t in wl.rope_tables(S))
+    nbytes = 4 * B * H * S * 64 * 2 + 2 * S * 64 * 4
+    out = {}
+    for name in ("fwd", "bwd"):
+        call = (lambda: ext.rope_fwd(q, k, cos, sin)) if name == "fwd" else \
+               (lambda: ext.rope_bwd(q, k, cos, sin, q, k))
+        for _ in range(3):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / n * 1e3
+        gbs = nbytes / (us / 1e6) / 1e9
+        out[name] = {"us": round(us, 2), "gb_s": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_GBS, 4)}
+    out["bytes_per_call"] = nbytes
+    return out
+
+
 def dropout_steps(torch, ext, q, k, v, do, scale, stream, step_flops, p=0.1, n=10):
     """The real-training setting (attention dropout 0.1): fwd+bwd through the
     binding with the backward hashing again, and with the forward's keep-bit
@@ -584,6 +614,7 @@ def main():
                           "flush_mb": 512, "sample": "median of 10 steps, each after a 512 MB device write"}}
     if not args.no_dropout:
         timing["dropout"] = dropout_steps(torch, ext, q, k, v, do, scale, stream, step_flops)
+    timing["rope"] = rope_timing(torch, ext, B, H, S, stream)
 
     result = {
         "metric": METRIC,

@@ -389,3 +389,52 @@ def test_rope_bitwise_vs_oracle(fa):
     for got, gg in ((dq, gq), (dk, gk)):
         ref = orc.rope_bwd(gg.numpy(), cos.numpy(), sin.numpy())
         assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_rope_scalar_path_bitwise(fa):
+    """Rows only 4-byte aligned (base offset by two halves, strides not multiples of 8):
+    the C ABI takes the scalar RoPE kernel; forward and backward still bitwise equal to
+    the oracle."""
+    say("case rope scalar path (4-byte aligned rows)")
+    B, S, H = 2, 100, 3
+    g = torch.Generator().manual_seed(6)
+    buf = torch.randn(B, S, H, 66, generator=g).half()
+    q = buf[..., 2:].transpose(1, 2)                           # (B,H,S,64), base +4 bytes, stride 66
+    kbuf = torch.randn(B, S, H, 66, generator=g).half()
+    k = kbuf[..., 2:].transpose(1, 2)
+    cos, sin = wl.rope_tables(S)
+    qd, kd = buf.to(DEV)[..., 2:].transpose(1, 2), kbuf.to(DEV)[..., 2:].transpose(1, 2)
+    assert qd.data_ptr() % 16 == 4 and qd.stride(1) % 8 != 0
+    ext = fa.extension()
+    qo, ko = ext.rope_fwd(qd, kd, cos.to(DEV), sin.to(DEV))
+    torch.cuda.synchronize()
+    for got, x in ((qo, q), (ko, k)):
+        ref = orc.rope_fwd(x.contiguous().numpy(), cos.numpy(), sin.numpy())
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+    dq, dk = ext.rope_bwd(qd, kd, cos.to(DEV), sin.to(DEV), qd, kd)
+    torch.cuda.synchronize()
+    for got, x in ((dq, q), (dk, k)):
+        ref = orc.rope_bwd(x.contiguous().numpy(), cos.numpy(), sin.numpy())
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("layout", ["fused_qkv", "bhsd"])
+def test_rope_config2_shape_bitwise(fa, layout):
+    """The vector RoPE kernel at config-2 shape (B=8 H=12 S=4096) in train.py's fused-qkv
+    layout and in contiguous (B,H,S,D): bitwise equal to the eager fp32 expression."""
+    say(f"case rope config-2 shape {layout}")
+    B, S, H = 8, 4096, 12
+    g = torch.Generator().manual_seed(7)
+    if layout == "fused_qkv":
+        qkv = torch.randn(B, S, 3 * H * 64, generator=g).half().to(DEV)
+        q, k, _ = (t.view(B, S, H, 64).transpose(1, 2) for t in qkv.chunk(3, dim=-1))
+    else:
+        q, k = (torch.randn(B, H, S, 64, generator=g).half().to(DEV) for _ in range(2))
+    cos, sin = (t.to(DEV) for t in wl.rope_tables(S))
+    qo, ko = fa.extension().rope_fwd(q, k, cos, sin)
+    c, s_ = cos[None, None], sin[None, None]
+    rot = lambda x: torch.cat((-x[..., 32:], x[..., :32]), dim=-1)
+    for got, x in ((qo, q), (ko, k)):
+        ref = (x.float() * c + rot(x.float()) * s_).half()
+        assert torch.equal(got, ref)
+

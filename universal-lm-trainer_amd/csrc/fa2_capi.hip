@@ -437,6 +437,15 @@ int fa2_rope_f16(const fa2_rope_params *p, int32_t backward, void *stream) {
     a.cs0 = p->cs_stride;
     a.sn0 = p->sn_stride;
     a.B = p->B; a.H = p->H; a.S = p->S;
+    {
+        const int64_t *st[4] = {p->q_stride, p->k_stride, p->qo_stride, p->ko_stride};
+        int64_t half_strides = 0;   // fp16 strides: multiples of 8 keep 16-byte rows
+        for (const int64_t *x : st) half_strides |= x[0] | x[1] | x[2];
+        const uintptr_t ptrs = reinterpret_cast<uintptr_t>(p->q) | reinterpret_cast<uintptr_t>(p->k) |
+                               reinterpret_cast<uintptr_t>(p->qo) | reinterpret_cast<uintptr_t>(p->ko) |
+                               reinterpret_cast<uintptr_t>(p->cos) | reinterpret_cast<uintptr_t>(p->sin);
+        a.vec16 = (ptrs & 15u) == 0 && (half_strides & 7) == 0 && ((p->cs_stride | p->sn_stride) & 3) == 0;
+    }
     const hipError_t e = fa2::launch_rope(a, backward != 0, (hipStream_t)stream);
     if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "rope launch: %s", hipGetErrorString(e));
     return FA2_OK;

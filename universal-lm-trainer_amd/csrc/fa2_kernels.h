@@ -68,6 +68,9 @@ struct RopeArgs {
     int64_t qsb, qsh, qss, ksb, ksh, kss, oqb, oqh, oqs, okb, okh, oks;
     int64_t cs0, sn0;
     int B, H, S;
+    // Every row pointer (q, k, qo, ko, cos, sin bases and strides) 16-byte
+    // aligned: the vector kernel; otherwise the 4-byte one.
+    bool vec16;
 };
 
 // Launchers; each returns the hipError_t of its launch.
