@@ -249,38 +249,32 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     return {dq, dk, dv};
 }
 
-bool is_dense(at::IntArrayRef sizes, at::IntArrayRef strides) {
-    int64_t need = 1, numel = 1;
-    for (size_t i = 0; i < sizes.size(); ++i) {
-        numel *= sizes[i];
-        need += (sizes[i] - 1) * strides[i];
-    }
-    return need == numel;
-}
-
-// Output layout of the eager path (fast_ops.cu:142-150): keep a dense input's
-// strides, (B,S,H,D) order for fused-qkv views, contiguous otherwise.
+// RoPE outputs get the memory order the eager expression x*cos + rotate_half(x)*sin
+// would give them (reference @ None: fast_ops.cu:142-150): an input that fills
+// its storage span keeps its own layout; a head-interleaved view (q or k of
+// the fused qkv projection: heads adjacent, positions H*64 or more apart)
+// becomes a packed (B, S, H, 64) tensor; any other view a packed (B, H, S, 64) one.
 std::vector<int64_t> rope_out_strides(const torch::Tensor &x) {
-    if (is_dense(x.sizes(), x.strides())) return x.strides().vec();
-    const int64_t B = x.size(0), H = x.size(1), S = x.size(2), D = x.size(3);
-    (void)B;
-    if (x.stride(1) == D && x.stride(2) >= H * D) return {S * H * D, D, H * D, 1};
+    if (x.is_non_overlapping_and_dense()) return x.strides().vec();
+    const int64_t H = x.size(1), S = x.size(2), D = x.size(3);
+    const bool heads_inner = x.stride(1) == D && x.stride(2) >= H * D;
+    if (heads_inner) return {S * H * D, D, H * D, 1};
     return {H * S * D, S * D, D, 1};
 }
 
+// Eligibility of the fused RoPE ops, each failure with its own message.
 void rope_check(const torch::Tensor &q, const torch::Tensor &k, const torch::Tensor &cos, const torch::Tensor &sin) {
-    TORCH_CHECK(q.is_cuda() && k.is_cuda(), "rope: inputs must be on the GPU");
-    TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf, "rope: fp16 only");
-    TORCH_CHECK(q.dim() == 4 && q.size(3) == 64, "rope: head_dim must be 64");
-    TORCH_CHECK(k.device() == q.device(), "rope: q/k device mismatch");
-    TORCH_CHECK(q.sizes() == k.sizes(), "rope: q/k shape mismatch");
-    TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1, "rope: last dim must be contiguous");
-    TORCH_CHECK(cos.is_cuda() && sin.is_cuda() && cos.dtype() == torch::kFloat && sin.dtype() == torch::kFloat,
-                "rope: cos/sin must be fp32 on the GPU");
-    TORCH_CHECK(cos.device() == q.device() && sin.device() == q.device(), "rope: cos/sin device mismatch");
-    TORCH_CHECK(cos.dim() == 2 && cos.size(0) == q.size(2) && cos.size(1) == 64, "rope: cos/sin must be [S, 64]");
-    TORCH_CHECK(cos.sizes() == sin.sizes(), "rope: cos/sin shape mismatch");
-    TORCH_CHECK(cos.stride(1) == 1 && sin.stride(1) == 1, "rope: cos/sin last dim must be contiguous");
+    auto need = [](bool ok, const char *what) { TORCH_CHECK(ok, "fused RoPE: ", what); };
+    need(q.is_cuda() && k.is_cuda() && k.device() == q.device(), "q and k must be on one GPU");
+    need(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf, "q and k must be fp16");
+    need(q.dim() == 4 && q.size(3) == 64 && q.sizes() == k.sizes(), "q and k must both be [B, H, S, 64]");
+    need(q.stride(3) == 1 && k.stride(3) == 1, "the head dimension of q and k must be unit-stride");
+    need(cos.is_cuda() && sin.is_cuda() && cos.device() == q.device() && sin.device() == q.device(),
+         "cos and sin must be on q's GPU");
+    need(cos.dtype() == torch::kFloat && sin.dtype() == torch::kFloat, "cos and sin must be fp32");
+    need(cos.dim() == 2 && cos.size(0) == q.size(2) && cos.size(1) == 64 && cos.sizes() == sin.sizes(),
+         "cos and sin must be [S, 64] with q's S");
+    need(cos.stride(1) == 1 && sin.stride(1) == 1, "cos and sin rows must be unit-stride");
 }
 
 std::vector<torch::Tensor> rope_run(const torch::Tensor &x, const torch::Tensor &y, const torch::Tensor &cos,
@@ -320,10 +314,8 @@ std::vector<torch::Tensor> rope_fwd(torch::Tensor q, torch::Tensor k, torch::Ten
 std::vector<torch::Tensor> rope_bwd(torch::Tensor dqo, torch::Tensor dko, torch::Tensor cos, torch::Tensor sin,
                                     torch::Tensor q, torch::Tensor k) {
     rope_check(q, k, cos, sin);
-    TORCH_CHECK(dqo.sizes() == q.sizes() && dko.sizes() == k.sizes(), "rope_bwd: grad shape");
-    TORCH_CHECK(dqo.is_cuda() && dko.is_cuda() && dqo.dtype() == torch::kHalf && dko.dtype() == torch::kHalf,
-                "rope_bwd: grads must be fp16 on the GPU");
-    TORCH_CHECK(dqo.stride(3) == 1 && dko.stride(3) == 1, "rope_bwd: grad last dim contiguous");
+    rope_check(dqo, dko, cos, sin);   // the incoming gradients obey the same rules
+    TORCH_CHECK(dqo.sizes() == q.sizes(), "fused RoPE backward: gradients must have q's shape");
     return rope_run(dqo, dko, cos, sin, q, k, true);
 }
 
