@@ -96,70 +96,65 @@ def read_traffic(kernel):
 
 
 class ClockSampler:
-    """Samples the GPU's graphics clock from the SMU metrics table (amdsmi
-    gpu_metrics: current_gfxclks per XCD where reported, else current_gfxclk)
-    every `period` seconds on a background thread while a timed region runs;
-    the median of the samples is the sustained clock reported beside the
-    result.  Unavailable metrics leave the report empty, never the bench."""
+    """The GPU's shader clock while the timed steps run.  A one-wave probe
+    kernel (lib/libfa2_clock_probe.so) on a second stream, launched just
+    before the steps it watches, reads s_memtime (its CU's clock cycles) and
+    s_memrealtime (the constant wall clock) at both ends of a window that
+    lies inside them: cycles / wall time = the mean clock of that CU over the
+    window.  Its wave holds a few registers of one SIMD, which keeps one
+    attention workgroup of 512 off that CU meanwhile; steps running beside it
+    take ~6% longer, so it runs beside extra steps, never the timed ones.  (amdsmi's gpu_metrics
+    on these boxes do not update under load, so they are not used.)"""
 
-    def __init__(self, torch, period=0.001):
-        import threading
-        self.period, self.samples, self.error, self.h = period, [], None, None
-        self._stop = threading.Event()
-        self._thread = None
+    def __init__(self, torch, window_s):
+        import ctypes as ct
+        self.torch, self.window_s, self.error, self.lib = torch, window_s, None, None
         try:
-            import amdsmi
-            amdsmi.amdsmi_init()
-            handles = amdsmi.amdsmi_get_processor_handles()
-            want = getattr(torch.cuda.get_device_properties(0), "pci_bus_id", None)
-            self.h = handles[0]
-            for h in handles:
-                bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)
-                if want is not None and int(bdf.split(":")[1], 16) == int(want):
-                    self.h = h
-            self._amdsmi = amdsmi
-            self._read()
-        except Exception as e:  # noqa: BLE001 -- any failure only disables the clock report
-            self.error, self.h = f"{type(e).__name__}: {e}", None
-
-    def _read(self):
-        m = self._amdsmi.amdsmi_get_gpu_metrics_info(self.h)
-        vals = [c for c in (m.get("current_gfxclks") or []) if isinstance(c, int) and 0 < c < 0xFFFF]
-        if not vals and isinstance(m.get("current_gfxclk"), int) and 0 < m["current_gfxclk"] < 0xFFFF:
-            vals = [m["current_gfxclk"]]
-        return sum(vals) / len(vals) if vals else None
-
-    def _run(self):
-        while not self._stop.wait(self.period):
-            try:
-                v = self._read()
-            except Exception as e:  # noqa: BLE001
-                self.error = f"{type(e).__name__}: {e}"
-                return
-            if v is not None:
-                self.samples.append(v)
+            lib = ct.CDLL(os.path.join(PKG, "lib", "libfa2_clock_probe.so"))
+            lib.fa2_clock_probe_launch.argtypes = [ct.c_void_p, ct.c_int64, ct.c_void_p]
+            lib.fa2_clock_probe_launch.restype = ct.c_int
+            lib.fa2_clock_probe_wall_hz.restype = ct.c_int64
+            self.lib, self.hz = lib, lib.fa2_clock_probe_wall_hz()
+            self.buf = torch.zeros(2, dtype=torch.int64, device="cuda")
+            self.stream = torch.cuda.Stream()
+        except OSError as e:
+            self.error = f"clock probe library not loaded: {e}"
 
     def __enter__(self):
-        import threading
-        if self.h is not None:
-            self._thread = threading.Thread(target=self._run, daemon=True)
-            self._thread.start()
+        import ctypes as ct
+        if self.lib is not None and self.hz > 0:
+            ticks = max(1, int(self.window_s * self.hz))
+            rc = self.lib.fa2_clock_probe_launch(ct.c_void_p(self.buf.data_ptr()), ticks,
+                                                 ct.c_void_p(self.stream.cuda_stream))
+            if rc != 0:
+                self.error = f"probe launch failed ({rc})"
         return self
 
     def __exit__(self, *exc):
-        self._stop.set()
-        if self._thread is not None:
-            self._thread.join(timeout=1.0)
+        self.torch.cuda.synchronize()
 
     def report(self):
-        if not self.samples:
-            return {"mhz_median": None, "samples": 0,
-                    "source": f"amdsmi gpu_metrics unavailable ({self.error or 'no samples'})"}
-        return {"mhz_median": round(statistics.median(self.samples), 1),
-                "mhz_min": round(min(self.samples), 1), "mhz_max": round(max(self.samples), 1),
-                "samples": len(self.samples),
-                "source": "amdsmi gpu_metrics current_gfxclk(s) (mean over XCDs), sampled every "
-                          f"{self.period * 1e3:.0f} ms during the timed steps"}
+        if self.error or self.lib is None:
+            return {"mhz": None, "source": self.error or "unavailable"}
+        cycles, wall = (int(x) for x in self.buf.tolist())
+        if wall <= 0:
+            return {"mhz": None, "source": "probe did not run"}
+        return {"mhz": round(cycles / wall * self.hz / 1e6, 1), "window_ms": round(wall / self.hz * 1e3, 3),
+                "source": "s_memtime / s_memrealtime of a one-wave probe kernel on a second stream whose "
+                          "window lies inside the watched steps (lib/libfa2_clock_probe.so)"}
+
+
+def clock_over_steps(torch, step, ms_per_step, n=10):
+    """The clock during n further steps identical to the timed ones (which run
+    without the probe: a kernel on a second stream slows them by ~6% on this
+    box), probe window 80% of their expected length."""
+    clock = ClockSampler(torch, 0.8 * n * ms_per_step / 1e3)
+    with clock:
+        for _ in range(n):
+            step()
+    out = clock.report()
+    out["sample"] = f"{n} further steps after the timed ones, the probe running beside them"
+    return out
 
 
 def cpu_baseline():
@@ -364,21 +359,22 @@ def decoder_step(args, torch, fa):
         scaler.update()
         return loss
 
+    tw = time.perf_counter()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    warm_s = (time.perf_counter() - tw) / max(args.warmup, 1)
     rec[0] = True
     sev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    clock = ClockSampler(torch)
-    with clock:
-        t0 = time.perf_counter()
-        sev[0].record()
-        for i in range(args.steps):
-            loss = step()
-            sev[i + 1].record()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    sev[0].record()
+    for i in range(args.steps):
+        loss = step()
+        sev[i + 1].record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
     rec[0] = False
+    clock = clock_over_steps(torch, step, ms_per_step=warm_s * 1e3, n=3)
     attn_ms = sum(a.elapsed_time(b) for a, b in spans) / args.steps
     assert len(spans) == 2 * L * args.steps, len(spans)
     attn_flops = dec.step_flops_attention(B, S, n_layers=L)
@@ -405,7 +401,7 @@ def decoder_step(args, torch, fa):
                  "attention_share": round(attn_ms / ms_per_step, 4),
                  "approx_model_tflops": round(dec.approx_step_flops(B, S) / (ms_per_step / 1e3) / 1e12, 1),
                  "last_loss": round(float(loss), 4)},
-        "clock": clock.report(),
+        "clock": clock,
         "parity": parity,
     }
 
@@ -566,16 +562,15 @@ def main():
         step()
     torch.cuda.synchronize()
     sev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    clock = ClockSampler(torch)
-    with clock:
-        t0 = time.perf_counter()
-        sev[0].record(stream)
-        for i in range(args.steps):
-            step()
-            sev[i + 1].record(stream)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    sev[0].record(stream)
+    for i in range(args.steps):
+        step()
+        sev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
     step_ms = [sev[i].elapsed_time(sev[i + 1]) for i in range(args.steps)]
+    clock = clock_over_steps(torch, step, ms_per_step=statistics.median(step_ms))
     ms_per_step = statistics.median(step_ms)
     value = step_flops / (ms_per_step / 1e3) / 1e12
     wall_ms = elapsed / args.steps * 1e3
@@ -638,7 +633,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(dom)},
         "kernels": kernels,
         "timing": timing,
-        "clock": clock.report(),
+        "clock": clock,
         "parity": parity,
     }
     if not args.no_cpu:

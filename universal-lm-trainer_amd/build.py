@@ -8,7 +8,9 @@ Produces, next to this file under ``lib/``:
     that C ABI (g++, linked with an ``$ORIGIN`` rpath);
   * ``probe_dq_atomics`` -- a stand-alone measurement of the fp32-atomic dQ
     accumulation traffic a fused backward would issue (the evidence behind
-    the split dQ pass), run under rocprofv3.
+    the split dQ pass), run under rocprofv3;
+  * ``libfa2_clock_probe.so`` -- bench.py's in-process clock reading (a
+    one-wave s_memtime / s_memrealtime probe; not part of the C ABI).
 
 Run ``python universal-lm-trainer_amd/build.py`` (or ``__graft_entry__.build()``).
 No GPU is needed: hipcc cross-compiles for gfx950.
@@ -119,11 +121,25 @@ def build_probe(verbose=False):
     return probe_path()
 
 
+def clock_probe_path():
+    return os.path.join(LIB, "libfa2_clock_probe.so")
+
+
+def build_clock_probe(verbose=False):
+    tmp = clock_probe_path() + ".tmp"
+    out = _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "clock_probe.hip"), "-o", tmp])
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, clock_probe_path())
+    return clock_probe_path()
+
+
 def build(verbose=False):
     build_library(verbose)
     build_extension(verbose)
     build_probe(verbose)
-    return lib_path(), ext_path(), probe_path()
+    build_clock_probe(verbose)
+    return lib_path(), ext_path(), probe_path(), clock_probe_path()
 
 
 if __name__ == "__main__":

@@ -788,7 +788,7 @@ static_assert(KP_NST >= 4 && KP_NST <= 6, "dK/dV stages");
 // workgroup's keys (4 runs of 32 words), moved into LDS by wave 1; each lane
 // tests one bit position of the words of its 16 query rows.
 template <bool CAUSAL, bool DROPOUT, bool FOLD, bool DMASK>
-__global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
+__device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, const int bh) {
     static_assert(!(FOLD && DROPOUT), "the folded row terms assume no dropout");
     static_assert(!DMASK || DROPOUT, "keep-bit words only with dropout");
     __shared__ __attribute__((aligned(16))) h8 sQD[KP_NST][2][KP_QT * 8];   // Q, dO tiles (4 KB each)
@@ -805,9 +805,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
     const int lane = tid & 63, c = lane & 31, g2 = lane >> 5;
     const int S = a.S;
     const int BH = a.B * a.H;
-    const int L = blockIdx.x;
-    const int kblk = L / BH;              // key block 0 first: the heaviest under the causal mask
-    const int bh = L - kblk * BH;
     const int b = bh / a.H, h = bh - b * a.H;
 
     const _Float16 *Qp = a.q + b * a.qsb + h * a.qsh;
@@ -1197,6 +1194,42 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
                    ((a.dvsb | a.dvsh | a.dvss) & 7) == 0);
 }
 
+// The dK/dV pass: workgroup L owns key blocks kp and nkb - 1 - kp of one
+// (b, h) (the middle block alone when nkb is odd), run one after the other:
+// under the causal mask their query ranges add up to the same length for
+// every pair, so all workgroups carry equal work.  Without the mask, and
+// with dropout, a workgroup owns one block.  With B*H a multiple of 8,
+// workgroups are numbered so that the 8 XCDs (blockIdx % 8) each take whole
+// heads, head after head: the workgroups one XCD runs at a time share a few
+// heads' Q / dO rows in its L2.
+template <bool CAUSAL, bool DROPOUT, bool FOLD, bool DMASK>
+__global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
+    const int BH = a.B * a.H;
+    const int nkb = (a.S + KP_KWG - 1) / KP_KWG;
+    // (With dropout the second copy of the block's code would spill.)
+    const bool pair = CAUSAL && !DROPOUT && a.dkv_pair;
+    const int nwg_head = pair ? (nkb + 1) / 2 : nkb;   // workgroups per head
+    const int L = blockIdx.x;
+    int j, bh;
+    if (pair && (BH & 7) == 0) {
+        const int xcd = L & 7, i = L >> 3;
+        bh = 8 * (i / nwg_head) + xcd;
+        j = i - (i / nwg_head) * nwg_head;
+    } else {
+        j = L / BH;
+        bh = L - j * BH;
+    }
+    // j = 0: key block 0, the heaviest under the causal mask, first.
+    dkv_block<CAUSAL, DROPOUT, FOLD, DMASK>(a, j, bh);
+    if (pair && nkb - 1 - j != j) {
+        // The first block's dK/dV staging reads must finish before the second
+        // block's transfers land in the same LDS.  (Two inlined copies of the
+        // block: a loop over both keeps values live across them and spills.)
+        lds_barrier();
+        dkv_block<CAUSAL, DROPOUT, FOLD, DMASK>(a, nkb - 1 - j, bh);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st) {
@@ -1244,9 +1277,12 @@ static void launch_dkv_t(const BwdArgs &a, bool causal, bool dropout, hipStream_
     }
 }
 
-hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+hipError_t launch_bwd_dkv(const BwdArgs &a_in, bool causal, bool dropout, hipStream_t st) {
+    BwdArgs a = a_in;
+    a.dkv_pair = causal && !dropout;
     const int nkblk = (a.S + KP_KWG - 1) / KP_KWG;
-    const dim3 grid((unsigned)(nkblk * a.B * a.H)), block(256);
+    const int nwg = a.dkv_pair ? (nkblk + 1) / 2 : nkblk;
+    const dim3 grid((unsigned)(nwg * a.B * a.H)), block(256);
     // The folded row terms need -lse2/scale2 finite (|lse2| < 3e18 at this bound).
     const bool fold = !dropout && a.scale2 >= 1e-20f;
     const bool dmask = dropout && a.drop_mask != nullptr;

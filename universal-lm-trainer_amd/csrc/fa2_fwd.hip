@@ -8,17 +8,25 @@
 // tiles, causal tiles past the diagonal skipped, the denominator summed from
 // the un-dropped P, O = acc / l with l == 0 -> 0, LSE in natural log.
 //
-// Work decomposition (one workgroup = 4 waves = 128 queries of one (b, h)):
-//   * each wave owns 32 queries; their Q^T operands (16 x 32 fp16 per
-//     d-step) stay in registers for the whole kernel;
+// Work decomposition (one workgroup = 4 waves of one (b, h)):
+//   * without dropout or key slices (the training path at p = 0 and most
+//     inference calls), each wave owns 64 queries, two 32-query blocks: every
+//     K and V operand fragment read from LDS feeds the MFMAs of both blocks,
+//     and the tile loop runs in order (scores, softmax, P V) -- the other
+//     workgroup's wave on the same SIMD overlaps its matrix and vector work;
+//   * with dropout or key slices, each wave owns 32 queries and the tile loop
+//     is software pipelined as described below;
+//   * a wave's Q^T operands (16 x 32 fp16 per d-step and block) stay in
+//     registers for the whole kernel;
 //   * key tiles of 64 keys are moved global -> LDS by the waves' direct
 //     transfers (global_load_lds, no register staging; a scalar tile base
 //     plus fixed 32-bit lane offsets) into XOR-swizzled tiles, four stages
-//     deep (three resident, one in flight); K feeds the A operand of
+//     deep (pipelined loop: three resident, one in flight; in-order loop: one
+//     read, three in flight); K feeds the A operand of
 //     S^T = K Q^T with 16-byte reads, V feeds the A operand of O^T = V^T P^T
 //     through transposing ds_read_b64_tr_b16 reads, both free of LDS bank
 //     conflicts;
-//   * the tile loop is software pipelined: step t issues the P V MFMAs of
+//   * the pipelined loop: step t issues the P V MFMAs of
 //     tile t-1 and the score MFMAs of tile t+1 while the VALU forms P of
 //     tile t, in chunks that pair two MFMAs with four exponentials;
 //   * S^T accumulators give each lane one query and 32 keys, so the row max
@@ -46,11 +54,13 @@ namespace {
 constexpr int NW = FA2_FWD_NW;     // waves per workgroup (4 or 8)
 constexpr int TPW = 8 / NW;        // 1 KB tile transfers per wave and tensor
 constexpr int KT = 64;             // keys per tile
-#ifndef FA2_FWD_QB
-#define FA2_FWD_QB 1
-#endif
-constexpr int QB = FA2_FWD_QB;     // 32-query blocks per wave (1: two waves per SIMD; 2: one)
-constexpr int QWG = NW * 32 * QB;  // queries per workgroup
+// 32-query blocks per wave (template parameter QBT of fwd_kernel):
+//   1: the software-pipelined step below (two tiles' matrix work beside one
+//      tile's softmax in every wave);
+//   2: each K / V operand fragment read from LDS feeds both query blocks, and
+//      the tile loop is not pipelined inside the wave (scores, softmax, PV in
+//      order): the other wave on the SIMD overlaps it.
+constexpr int qwg_of(int qbt) { return NW * 32 * qbt; }   // queries per workgroup
 #ifndef FA2_FWD_NST
 #define FA2_FWD_NST 4
 #endif
@@ -64,9 +74,14 @@ constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <
 //
 // DMASK (dropout, no key slices): each lane also stores its tile's 32 keep
 // bits as one word of a.drop_mask (dmask_word layout), for the backward.
-template <bool CAUSAL, bool DROPOUT, bool SPLIT, bool DMASK>
-__global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs a) {
+template <bool CAUSAL, bool DROPOUT, bool SPLIT, bool DMASK, int QBT>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
+    constexpr int QB = QBT;
+    constexpr int QWG = qwg_of(QBT);
+    constexpr bool NOPIPE = QBT == 2;
+    static_assert(QBT == 1 || QBT == 2, "one or two query blocks per wave");
     static_assert(!DMASK || (DROPOUT && !SPLIT && QB == 1 && NST == 4), "keep-bit words: one store per tile");
+    static_assert(!NOPIPE || NST == 4, "the unpipelined loop's waits assume four stages");
     // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
     __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
 
@@ -416,6 +431,65 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // are in flight.  The barrier after step t publishes tile t+2 and frees
     // the stage of tile t-1 for tile t+NST-1.
     static_assert(NST == 4 || NST == 5, "three resident tiles plus one or two in flight");
+    if constexpr (NOPIPE) {
+        // Step t reads only tile t, so tiles t+1 .. t+3 may be in flight
+        // meanwhile: tile 3 goes out now, and each tile end waits for the
+        // next tile only (2*TPW transfers per tile and wave) and refills the
+        // stage just read with tile t+4.
+        if (NST - 1 < ntiles) issue(NST - 1);
+        auto wait_pending = [&](int n) FA2_INLINE {   // at most n tiles' transfers in flight
+            if (n <= 0) vm_wait<0>();
+            else if (n == 1) vm_wait<2 * TPW>();
+            else if (n == 2) vm_wait<4 * TPW>();
+            else vm_wait<6 * TPW>();
+        };
+        wait_pending(min(NST - 1, ntiles - 1));
+        lds_barrier();
+        f16x s[QB][2];
+        h8 p[QB][2][2];
+        for (int t = 0; t < ntiles; ++t) {
+            const int k0 = kbase + t * KT;
+            const int stage = stage_of(t);
+            if (t <= tlast) {
+                s_mm(stage, s);
+                if (need_mask(k0)) {
+                    FA2_COLD_BRANCH();
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) mask(qb, k0, s[qb]);
+                }
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    float rs = p_form(s[qb], msc[qb], p[qb]);
+                    if (__any(!(rs <= P_SUM_LIMIT))) {
+                        // The cold path on the live scores: true row max,
+                        // rescale of O and l, P again (on the first tile msc
+                        // is -inf and it always runs).
+                        FA2_COLD_BRANCH();
+                        float mx = s[qb][0][0];
+#pragma unroll
+                        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
+                        mx = fmaxf(mx, xor32(mx));
+                        const float mnew = fmaxf(msc[qb], mx * scale2);
+                        const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc[qb] - mnew);
+                        msc[qb] = mnew;
+                        l[qb] *= alpha;
+#pragma unroll
+                        for (int db = 0; db < 2; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+                        rs = p_form(s[qb], (mnew == -INFINITY) ? 0.f : mnew, p[qb]);
+                    }
+                    l[qb] += rs;
+                }
+                pv(stage, p);
+            }
+            wait_pending(min(NST - 2, ntiles - 2 - t));   // tile t+1 landed
+            lds_barrier();                                   // every wave is done with tile t
+            if (t + NST < ntiles) issue(t + NST);
+        }
+    } else {
     // Tiles 0 and 1 have landed once at most the transfers of tiles
     // 2 .. NST-2 are pending (4 per tile and wave).
     if (NST == 5 && ntiles >= 4) vm_wait<8>(); else if (ntiles >= 3) vm_wait<4>(); else vm_wait<0>();
@@ -525,6 +599,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
         general(t, s0, p0, s1, p1);
         if (t + 1 < ntiles) general(t + 1, s1, p1, s0, p0);
     }
+    }   // pipelined loop
 
     // Outputs leave the MFMA accumulators with each lane holding one query
     // and runs of 4 consecutive columns, so direct stores would touch 32 rows
@@ -532,7 +607,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW / QB) void fwd_kernel(const FwdArgs
     // through a private, XOR-swizzled slice of the tile stages instead (idle
     // now: every wave is past its last tile read and no transfer is in
     // flight), then stores whole rows with 16-byte lanes.
-    static_assert(sizeof(sKV) >= NW * QB * 8192, "output staging fits in the tile stages");
+    static_assert(sizeof(sKV) >= NW * QB * (SPLIT ? 8192 : 4096), "output staging fits in the tile stages");
     char *const stage_base = reinterpret_cast<char *>(&sKV[0][0][0]);
     if (SPLIT) {
         // Partial result of this slice: the O^T accumulator, the reference
@@ -764,25 +839,33 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_kernel(const FwdArgs a) {
 
 template <bool SPLIT>
 void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
-    const int nqblk = (a.S + QWG - 1) / QWG;
-    const dim3 grid((unsigned)(nqblk * a.B * a.H * (SPLIT ? a.nsplit : 1)));
     const dim3 block(NW * 64);
     // Keep-bit words only from the unsplit forward (the training path).
     const bool dmask = !SPLIT && dropout && a.drop_mask != nullptr;
+    // Without dropout or key slices: two query blocks per wave (2 to 3% faster
+    // than the pipelined single block); dropout keeps one block per wave, whose
+    // keep-bit words hold one query per lane.
+    const bool two = !SPLIT && !dropout;
+    const int nqblk = (a.S + (two ? qwg_of(2) : qwg_of(1)) - 1) / (two ? qwg_of(2) : qwg_of(1));
+    const dim3 grid((unsigned)(nqblk * a.B * a.H * (SPLIT ? a.nsplit : 1)));
     if (causal) {
         if (dmask)
-            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, !SPLIT>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, !SPLIT, 1>), grid, block, 0, st, a);
         else if (dropout)
-            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, false, 1>), grid, block, 0, st, a);
+        else if (two)
+            hipLaunchKernelGGL((fwd_kernel<true, false, false, false, 2>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((fwd_kernel<true, false, SPLIT, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<true, false, SPLIT, false, 1>), grid, block, 0, st, a);
     } else {
         if (dmask)
-            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, !SPLIT>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, !SPLIT, 1>), grid, block, 0, st, a);
         else if (dropout)
-            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, false, 1>), grid, block, 0, st, a);
+        else if (two)
+            hipLaunchKernelGGL((fwd_kernel<false, false, false, false, 2>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((fwd_kernel<false, false, SPLIT, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((fwd_kernel<false, false, SPLIT, false, 1>), grid, block, 0, st, a);
     }
 }
 

@@ -59,6 +59,8 @@ struct BwdArgs {
     // Dropout keep bits the forward wrote (dmask_word layout), or null: the
     // passes then evaluate the hash themselves.
     const uint32_t *drop_mask;
+    // dK/dV pass: one workgroup runs key blocks j and nkb - 1 - j (causal).
+    bool dkv_pair;
 };
 
 struct RopeArgs {
