@@ -13,7 +13,7 @@
 //   * bwd_dq_pipe_kernel: a workgroup owns 256 queries, keeps Q^T, dO^T, lse
 //     and delta of its queries in registers and streams key tiles (K, V
 //     row-major via LDS; K^T operands come from transposing ds_read_b64_tr_b16
-//     reads).  It also computes delta itself (the reference's pre-pass,
+//     reads), in order, three tiles in flight.  It also computes delta itself (the reference's pre-pass,
 //     bwd.cu:42-61) from the O and dO rows it holds and stores it for the
 //     dK/dV pass.  S^T and dP^T accumulators give each lane one query, so
 //     lse/delta are per-lane scalars and dS^T feeds the dQ^T = K^T dS^T MFMA
@@ -103,22 +103,23 @@ __global__ __launch_bounds__(256) void bwd_dq_convert_kernel(const BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ pass (+ delta), software pipelined
+// dQ pass (+ delta)
 // ---------------------------------------------------------------------------
 constexpr int DQ_NW = 4;
 constexpr int DQ_QB = 2;                    // 32-query blocks per wave
 constexpr int DQ_KT = 64;                   // keys per tile
 constexpr int DQ_QWG = DQ_NW * 32 * DQ_QB;  // 256 queries per workgroup
-constexpr int QP_NST = 4;   // LDS stages: key tiles t-1, t, t+1 resident, t+2 in flight
+constexpr int QP_NST = 4;   // LDS stages: key tile t read, t+1 .. t+3 in flight
 
-// 256 queries per workgroup, 64 per wave, 64-key tiles, cut into units
-// u = 4t + 2kb + qb: key block kb (32 keys) of key tile t against query block
-// qb (32 queries) of the wave.  Step u issues the dQ MFMAs of unit u-1 and
-// the S/dP MFMAs of unit u+1 while the VALU forms dS of unit u, so the
-// exponentials and the dS arithmetic run beside matrix work of the same wave.
-// A unit reads its K / V fragments from LDS itself rather than sharing them
-// between the two query blocks, which keeps two units in flight within 256
-// registers.
+// 256 queries per workgroup, 64 per wave (two 32-query blocks), 64-key tiles
+// taken 32 keys (kb) at a time, in order: S and dP of both query blocks from
+// one pass over the K / V row fragments (each fragment read from LDS feeds two
+// MFMAs), dS, then dQ of both blocks from one pass over the K^T fragments.
+// The loop is not pipelined inside the wave -- the other workgroup's wave on
+// the same SIMD overlaps its matrix and vector work -- so a step reads only
+// its own tile and three tiles stay in flight.  (A pipelined form that
+// interleaved neighbouring 32 x 32 units inside the wave, each reading its
+// fragments itself, was 2% slower at S = 4096 and 4% at S = 512.)
 //
 // DMASK (dropout with a.drop_mask): the keep bits come from the words the
 // forward wrote (two per query and key tile, moved into LDS with the tile)
@@ -266,16 +267,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         ones3 = g2 == 0 ? ones3_b8() : zero_b8();
     }
 
-    // End of tile t's third step: tile t+1 landed (tiles up to t+2 are issued,
-    // 4 transfers per tile and wave, 6 with DMASK), the barrier publishes it
-    // and frees the stage of tile t-1 (last read by step 4t), and tile t+3
-    // goes into it.
-    auto tile_end = [&](int t) FA2_INLINE {
-        if (t + 2 < ntiles) vm_wait<DMASK ? 6 : 4>(); else vm_wait<0>();
-        lds_barrier();
-        if (t + QP_NST - 1 < ntiles) issue(t + QP_NST - 1);
-    };
-
     // LDS read offsets: K / V rows 32*kb + c at logical chunk 2*st + g2, and
     // K^T through transposing reads (d block db, row half hi).
     int roff[4];
@@ -295,23 +286,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
                              32 * kb + 16 * hh);
     };
 
-    // S^T = K Q^T and dP^T = V dO^T of unit (stage, kb, qb).
-    auto sdp = [&](int stage, int kb, int qb, f16x &s, f16x &dp) FA2_INLINE {
-        if (!DROPOUT) dp = mfma32_bf16_first(ones3, dmb[qb]);
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const h8 ka = rrow(stage, 0, kb, st), va = rrow(stage, 1, kb, st);
-            s = st == 0 ? mfma32_first(ka, qf[qb][0]) : mfma32(ka, qf[qb][st], s);
-            dp = (st == 0 && DROPOUT) ? mfma32_first(va, dof[qb][0]) : mfma32(va, dof[qb][st], dp);
-        }
-    };
-    // dQ^T += K^T dS^T of unit (stage, kb, qb).
-    auto dq_mm = [&](int stage, int kb, int qb, const h8(&dsb)[2]) FA2_INLINE {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-            for (int db = 0; db < 2; ++db) dq[qb][db] = mfma32(trk(stage, kb, db, hh), dsb[hh], dq[qb][db]);
-    };
     // Keys past S and, causal, after the query -> -inf.  key = t*KT + 32*kb +
     // 4*g2 + (8*(r>>2) + (r&3)), compared as a constant against a per-lane bound.
     auto need_mask = [&](int t) FA2_INLINE {
@@ -355,107 +329,71 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         dsb[1] = acc_to_h8(x, 1);
     };
 
-    // Pipelined step: dS of unit (t, kb, qb) from (s_c, dp_c) into ds_c; the
-    // dQ MFMAs of the previous unit (stage sp, kbp, qbp, from ds_p); the S/dP
-    // MFMAs of the next unit (stage sn, kbn, qbn) into (s_n, dp_n).  Six
-    // chunks of two MFMAs (dQ for hh = 0, 1, then S/dP for d-steps 0..3), the
-    // operand reads of chunk i+1 issued in chunk i, elements 3,3,3,3,2,2.
-    auto step = [&](int t, int kb, int qb, const f16x &s_c, const f16x &dp_c, h8(&ds_c)[2], int sp, int kbp,
-                    int qbp, const h8(&ds_p)[2], int sn, int kbn, int qbn, f16x &s_n, f16x &dp_n) FA2_INLINE {
-        h8 n0 = trk(sp, kbp, 0, 0), n1 = trk(sp, kbp, 1, 0);
-        float x[16];
-        const uint32_t mw = keep_word(t, qb);
-#pragma unroll
-        for (int i = 0; i < 6; ++i) {
-            const h8 f0 = n0, f1 = n1;
-            if (i == 0) {
-                n0 = trk(sp, kbp, 0, 1);
-                n1 = trk(sp, kbp, 1, 1);
-            } else if (i < 5) {
-                n0 = rrow(sn, 0, kbn, i - 1);
-                n1 = rrow(sn, 1, kbn, i - 1);
-            }
-            if (i < 2) {
-                dq[qbp][0] = mfma32(f0, ds_p[i], dq[qbp][0]);
-                dq[qbp][1] = mfma32(f1, ds_p[i], dq[qbp][1]);
-                if (i == 1 && !DROPOUT) dp_n = mfma32_bf16_first(ones3, dmb[qbn]);
-            } else if (i == 2) {
-                s_n = mfma32_first(f0, qf[qbn][0]);
-                dp_n = DROPOUT ? mfma32_first(f1, dof[qbn][0]) : mfma32(f1, dof[qbn][0], dp_n);
-            } else {
-                s_n = mfma32(f0, qf[qbn][i - 2], s_n);
-                dp_n = mfma32(f1, dof[qbn][i - 2], dp_n);
-            }
-            const int elo = i < 4 ? 3 * i : 12 + 2 * (i - 4);
-            const int ehi = i < 3 ? 3 * i + 3 : 12 + 2 * (i - 3);
-#pragma unroll
-            for (int e = elo; e < ehi; ++e) {
-                x[e] = ds_of(s_c[e], dp_c[e], t, kb, qb, e, mw);
-                if (e & 1) {
-                    const f2 xx = {x[e - 1], x[e]};
-                    const h2 hd = __builtin_convertvector(xx, h2);
-                    // Consumed here: keeps the chunk's VALU work beside its MFMAs.
-                    asm volatile("" ::"v"(hd));
-                    ds_c[e >> 3][(e - 1) & 7] = hd[0];
-                    ds_c[e >> 3][e & 7] = hd[1];
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
     // Query block qb's units keep S, dP and dS in role qb (A: 0, B: 1).
     f16x sA, dpA, sB, dpB;
     h8 dsA[2], dsB[2];
-    // Tile 0 landed once at most the transfers of tiles 1 and 2 are pending.
-    if (ntiles >= 3) vm_wait<DMASK ? 12 : 8>(); else if (ntiles == 2) vm_wait<DMASK ? 6 : 4>(); else vm_wait<0>();
-    lds_barrier();
-    if (tlast >= 0) {
-        sdp(0, 0, 0, sA, dpA);
-        dsB[0] = zero_h8();   // tile 0's first step adds K * 0 for the (absent) unit before it
-        dsB[1] = zero_h8();
-        int t = 0;
-        for (; t < tlast; ++t) {
-            const int st = stage_of(t), sp = stage_of(t + QP_NST - 1), sn = stage_of(t + 1);
-            step(t, 0, 0, sA, dpA, dsA, t > 0 ? sp : st, 1, 1, dsB, st, 0, 1, sB, dpB);
-            step(t, 0, 1, sB, dpB, dsB, st, 0, 0, dsA, st, 1, 0, sA, dpA);
-            step(t, 1, 0, sA, dpA, dsA, st, 0, 1, dsB, st, 1, 1, sB, dpB);
-            tile_end(t);
-            step(t, 1, 1, sB, dpB, dsB, st, 1, 0, dsA, sn, 0, 0, sA, dpA);
+    {
+        // Step t reads only tile t: tiles t+1 .. t+3 may be in flight.  Tile 3
+        // goes out now; each tile end waits for the next tile only and
+        // refills the stage just read with tile t+4.
+        constexpr int TPT = DMASK ? 6 : 4;   // transfers per tile and wave
+        if (QP_NST - 1 < ntiles) issue(QP_NST - 1);
+        auto wait_pending = [&](int n) FA2_INLINE {
+            if (n <= 0) vm_wait<0>();
+            else if (n == 1) vm_wait<TPT>();
+            else if (n == 2) vm_wait<2 * TPT>();
+            else vm_wait<3 * TPT>();
+        };
+        wait_pending(min(QP_NST - 1, ntiles - 1));
+        lds_barrier();
+        for (int t = 0; t < ntiles; ++t) {
+            const int st = stage_of(t);
+            if (t <= tlast) {
+                const bool m = need_mask(t);
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    if (!DROPOUT) {
+                        dpA = mfma32_bf16_first(ones3, dmb[0]);
+                        dpB = mfma32_bf16_first(ones3, dmb[1]);
+                    }
+#pragma unroll
+                    for (int sti = 0; sti < 4; ++sti) {
+                        const h8 ka = rrow(st, 0, kb, sti), va = rrow(st, 1, kb, sti);
+                        sA = sti == 0 ? mfma32_first(ka, qf[0][0]) : mfma32(ka, qf[0][sti], sA);
+                        sB = sti == 0 ? mfma32_first(ka, qf[1][0]) : mfma32(ka, qf[1][sti], sB);
+                        dpA = (sti == 0 && DROPOUT) ? mfma32_first(va, dof[0][0]) : mfma32(va, dof[0][sti], dpA);
+                        dpB = (sti == 0 && DROPOUT) ? mfma32_first(va, dof[1][0]) : mfma32(va, dof[1][sti], dpB);
+                    }
+                    if (m) {
+                        FA2_COLD_BRANCH();
+                        mask(t, kb, 0, sA);
+                        mask(t, kb, 1, sB);
+                    }
+                    ds_form(t, kb, 0, sA, dpA, dsA);
+                    ds_form(t, kb, 1, sB, dpB, dsB);
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int db = 0; db < 2; ++db) {
+                            const h8 kt = trk(st, kb, db, hh);
+                            dq[0][db] = mfma32(kt, dsA[hh], dq[0][db]);
+                            dq[1][db] = mfma32(kt, dsB[hh], dq[1][db]);
+                        }
+                }
+            }
+            if (t < ntiles - 1) {
+                wait_pending(min(QP_NST - 2, ntiles - 2 - t));   // tile t+1 landed
+                lds_barrier();
+                if (t + QP_NST < ntiles) issue(t + QP_NST);
+            }
         }
-        // Tile tlast in serial order, masked where needed.
-        const int st = stage_of(t), sp = stage_of(t + QP_NST - 1);
-        const bool m = need_mask(t);
-        if (m) {
-            FA2_COLD_BRANCH();
-            mask(t, 0, 0, sA);
-        }
-        ds_form(t, 0, 0, sA, dpA, dsA);
-        if (t > 0) dq_mm(sp, 1, 1, dsB);
-        dq_mm(st, 0, 0, dsA);
-        sdp(st, 0, 1, sB, dpB);
-        if (m) mask(t, 0, 1, sB);
-        ds_form(t, 0, 1, sB, dpB, dsB);
-        dq_mm(st, 0, 1, dsB);
-        sdp(st, 1, 0, sA, dpA);
-        if (m) mask(t, 1, 0, sA);
-        ds_form(t, 1, 0, sA, dpA, dsA);
-        dq_mm(st, 1, 0, dsA);
-        sdp(st, 1, 1, sB, dpB);
-        if (m) mask(t, 1, 1, sB);
-        ds_form(t, 1, 1, sB, dpB, dsB);
-        dq_mm(st, 1, 1, dsB);
-        if (t < ntiles - 1) tile_end(t);
     }
-    // Tiles after this wave's last: keep joining the barriers and moving tiles.
-    for (int t = max(tlast + 1, 0); t < ntiles - 1; ++t) tile_end(t);
 
     // dQ rows leave through LDS (store_rows_f16).  The last tile has no
-    // barrier after it, so other waves may still read the stages of tiles
-    // ntiles-1 and ntiles-2; the other two stages are idle (their last
-    // reads precede the barrier of tile ntiles-2, and the last transfer went
-    // into the stage of tile ntiles-1): waves 0, 1 use stage ntiles % 4,
-    // waves 2, 3 stage (ntiles + 1) % 4, 4 KB per 32-query block.
+    // barrier after it, so other waves may still read the stage of tile
+    // ntiles-1; stages ntiles % 4 and (ntiles + 1) % 4 are idle (their last
+    // reads precede an earlier barrier, and every transfer has landed): waves
+    // 0, 1 use the first, waves 2, 3 the second, 4 KB per 32-query block.
     static_assert(QP_NST == 4 && DQ_QB == 2 && sizeof(sKV[0]) == 16384, "dQ staging layout");
     const float sc = a.scale;
     const bool dq16 = ((a.dqsb | a.dqsh | a.dqss) & 7) == 0;
@@ -723,7 +661,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int r = 8 * i + 4 * g2 + j;
-                    if (q0 + 32 * qb2 + r < S) atomicAddNoRet(accrow + r * HD, acc[4 * i + j]);
+                    if (q0 + 32 * qb2 + r < S)
+                        __hip_atomic_fetch_add(accrow + r * HD, acc[4 * i + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
         }
         if (t + 1 < ntiles) lstore(buf ^ 1);
