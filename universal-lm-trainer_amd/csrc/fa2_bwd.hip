@@ -1218,8 +1218,14 @@ static void launch_dkv_t(const BwdArgs &a, bool causal, bool dropout, hipStream_
 
 hipError_t launch_bwd_dkv(const BwdArgs &a_in, bool causal, bool dropout, hipStream_t st) {
     BwdArgs a = a_in;
-    a.dkv_pair = causal && !dropout;
     const int nkblk = (a.S + KP_KWG - 1) / KP_KWG;
+    // Key-block pairs (causal, no dropout) give every workgroup the same work,
+    // head after head per XCD.  That pays only when each XCD's share fills
+    // whole rounds of its 2*CUs/8 workgroup slots; otherwise the single
+    // blocks, heaviest first, pack the rounds better.
+    const int64_t bh = (int64_t)a.B * a.H, per_xcd = (nkblk + 1) / 2 * (bh / 8);
+    const int64_t xcd_slots = 2 * (int64_t)device_cus() / 8;
+    a.dkv_pair = causal && !dropout && bh % 8 == 0 && per_xcd > 0 && per_xcd % xcd_slots == 0;
     const int nwg = a.dkv_pair ? (nkblk + 1) / 2 : nkblk;
     const dim3 grid((unsigned)(nwg * a.B * a.H)), block(256);
     // The folded row terms need -lse2/scale2 finite (|lse2| < 3e18 at this bound).

@@ -82,6 +82,20 @@ int check_mask(const void *mask, size_t bytes, int32_t B, int32_t H, int32_t S, 
 
 }  // namespace
 
+namespace fa2 {
+int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;   // idempotent: racing first calls store the same value
+    }
+    return cached[dev];
+}
+}  // namespace fa2
+
 extern "C" {
 
 // keep iff (hash >> 8) * 2^-24 >= p  <=>  (hash >> 8) >= ceil(p * 2^24): p * 2^24

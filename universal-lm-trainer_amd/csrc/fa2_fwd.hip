@@ -843,9 +843,12 @@ void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     // Keep-bit words only from the unsplit forward (the training path).
     const bool dmask = !SPLIT && dropout && a.drop_mask != nullptr;
     // Without dropout or key slices: two query blocks per wave (2 to 3% faster
-    // than the pipelined single block); dropout keeps one block per wave, whose
-    // keep-bit words hold one query per lane.
-    const bool two = !SPLIT && !dropout;
+    // than the pipelined single block) when that still fills every slot of two
+    // workgroups per CU; otherwise (short query ranges: prefill chunks) one
+    // block per wave, for twice the workgroups.  Dropout keeps one block per
+    // wave, whose keep-bit words hold one query per lane.
+    const bool two = !SPLIT && !dropout &&
+                     (int64_t)((a.S + qwg_of(2) - 1) / qwg_of(2)) * a.B * a.H >= 2 * (int64_t)device_cus();
     const int nqblk = (a.S + (two ? qwg_of(2) : qwg_of(1)) - 1) / (two ? qwg_of(2) : qwg_of(1));
     const dim3 grid((unsigned)(nqblk * a.B * a.H * (SPLIT ? a.nsplit : 1)));
     if (causal) {

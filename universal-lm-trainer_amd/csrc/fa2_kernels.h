@@ -75,6 +75,10 @@ struct RopeArgs {
     bool vec16;
 };
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+// Launchers use it to size grids against the slots of two workgroups per CU.
+int device_cus();
+
 // Launchers; each returns the hipError_t of its launch.
 hipError_t launch_fwd(const FwdArgs &a, bool causal, bool dropout, hipStream_t st);
 // The forward over a.nsplit key slices (partials into a.part_o / a.part_ml), then their merge.
