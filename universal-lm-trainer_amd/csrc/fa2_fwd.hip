@@ -80,7 +80,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     constexpr int QWG = qwg_of(QBT);
     constexpr bool NOPIPE = QBT == 2;
     static_assert(QBT == 1 || QBT == 2, "one or two query blocks per wave");
-    static_assert(!DMASK || (DROPOUT && !SPLIT && QB == 1 && NST == 4), "keep-bit words: one store per tile");
+    static_assert(!DMASK || (DROPOUT && !SPLIT && NST == 4), "keep-bit words: the unsplit forward");
     static_assert(!NOPIPE || NST == 4, "the unpipelined loop's waits assume four stages");
     // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
     __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
@@ -302,6 +302,50 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // the cold path (scores recomputed from the K tile, so no score register
     // has to outlive P), dropout, and the running sum.
     uint32_t wpend = 0;   // DMASK: the keep word of the tile being finished
+    // Dropout on the P of query block qb, tile k0 (l already holds its
+    // un-dropped sum); returns the keep word (DMASK) of the lane's query.
+    auto drop_apply = [&](int qb, int k0, h8(&pb)[2][2]) FA2_INLINE -> uint32_t {
+        // l sums the un-dropped P; dropout then zeroes / rescales P.
+        // The keep decision selects the multiplier m = -1/(1-p) or +0, and
+        // each packed fp16 pair of P is scaled in place by two mixed-
+        // precision FMAs, v_fma_mixlo_f16 / v_fma_mixhi_f16: (-P) * m + 0
+        // in fp32 with P read as fp16 (op_sel_hi bit 1 of source 0; op_sel
+        // bit 1 picks its high half; "-" negates it) and m as fp32, the
+        // result rounded to fp16 into the low / high half.  That is one
+        // instruction per element instead of a widen, a multiply and half
+        // a repack.  m's sign bit is the keep bit: DMASK shifts it into
+        // the word (one funnel shift, v_alignbit_b32, per element), so
+        // element 16*kb + 8*hh + e lands on bit 31 - (16*kb + 8*hh + e).
+        uint32_t w = 0;
+        const uint32_t hrow = dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+                u4x pk = __builtin_bit_cast(u4x, pb[kb][hh]);
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    float m[2];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int e = 2 * e2 + j;
+                        const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
+                        const bool keep = dropout_keep_hashed(hrow ^ dropout_col_term(key), a.drop_thr);
+                        m[j] = keep ? -a.inv_keep : 0.f;
+                        if (DMASK) w = (w << 1) | (__builtin_bit_cast(uint32_t, m[j]) >> 31);
+                    }
+                    uint32_t r;
+                    asm("v_fma_mixlo_f16 %0, -%1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pk[e2]), "v"(m[0]));
+                    asm("v_fma_mixhi_f16 %0, -%1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                        : "+v"(r)
+                        : "v"(pk[e2]), "v"(m[1]));
+                    pk[e2] = r;
+                }
+                pb[kb][hh] = __builtin_bit_cast(h8, pk);
+            }
+        return w;
+    };
     auto softmax_tail = [&](int qb, int k0, int stage, h8(&pb)[2][2], float rs) FA2_INLINE {
         if (__any(!(rs <= P_SUM_LIMIT))) {
             FA2_COLD_BRANCH();
@@ -327,45 +371,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
             rs = p_form(s, (mnew == -INFINITY) ? 0.f : mnew, pb);
         }
         if (DROPOUT) {
-            // l sums the un-dropped P; dropout then zeroes / rescales P.
-            // The keep decision selects the multiplier m = -1/(1-p) or +0, and
-            // each packed fp16 pair of P is scaled in place by two mixed-
-            // precision FMAs, v_fma_mixlo_f16 / v_fma_mixhi_f16: (-P) * m + 0
-            // in fp32 with P read as fp16 (op_sel_hi bit 1 of source 0; op_sel
-            // bit 1 picks its high half; "-" negates it) and m as fp32, the
-            // result rounded to fp16 into the low / high half.  That is one
-            // instruction per element instead of a widen, a multiply and half
-            // a repack.  m's sign bit is the keep bit: DMASK shifts it into
-            // the word (one funnel shift, v_alignbit_b32, per element), so
-            // element 16*kb + 8*hh + e lands on bit 31 - (16*kb + 8*hh + e).
-            uint32_t w = 0;
-            const uint32_t hrow = dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh);
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    typedef uint32_t u4x __attribute__((ext_vector_type(4)));
-                    u4x pk = __builtin_bit_cast(u4x, pb[kb][hh]);
-#pragma unroll
-                    for (int e2 = 0; e2 < 4; ++e2) {
-                        float m[2];
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            const int e = 2 * e2 + j;
-                            const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
-                            const bool keep = dropout_keep_hashed(hrow ^ dropout_col_term(key), a.drop_thr);
-                            m[j] = keep ? -a.inv_keep : 0.f;
-                            if (DMASK) w = (w << 1) | (__builtin_bit_cast(uint32_t, m[j]) >> 31);
-                        }
-                        uint32_t r;
-                        asm("v_fma_mixlo_f16 %0, -%1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pk[e2]), "v"(m[0]));
-                        asm("v_fma_mixhi_f16 %0, -%1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-                            : "+v"(r)
-                            : "v"(pk[e2]), "v"(m[1]));
-                        pk[e2] = r;
-                    }
-                    pb[kb][hh] = __builtin_bit_cast(h8, pk);
-                }
+            const uint32_t w = drop_apply(qb, k0, pb);
             if (DMASK) wpend = w;   // stored by tile_end
         }
         l[qb] += rs;
@@ -447,6 +453,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         lds_barrier();
         f16x s[QB][2];
         h8 p[QB][2][2];
+        uint32_t wq[QB] = {};   // DMASK: the keep words of the tile (one per query block)
         for (int t = 0; t < ntiles; ++t) {
             const int k0 = kbase + t * KT;
             const int stage = stage_of(t);
@@ -482,12 +489,23 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
                         rs = p_form(s[qb], (mnew == -INFINITY) ? 0.f : mnew, p[qb]);
                     }
                     l[qb] += rs;
+                    if (DROPOUT) wq[qb] = drop_apply(qb, k0, p[qb]);
                 }
                 pv(stage, p);
             }
             wait_pending(min(NST - 2, ntiles - 2 - t));   // tile t+1 landed
             lds_barrier();                                   // every wave is done with tile t
             if (t + NST < ntiles) issue(t + NST);
+            if (DMASK && t <= tlast) {
+                // Stored after the tile's transfers: the count-based waits
+                // never count a store (one issued after the awaited loads only
+                // makes a wait longer).
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    const int q = qw0 + 32 * qb + c;
+                    if (q < S) a.drop_mask[dmask_word(bh, S, kbase / KT + t, g2, q)] = wq[qb];
+                }
+            }
         }
     } else {
     // Tiles 0 and 1 have landed once at most the transfers of tiles
@@ -842,31 +860,38 @@ void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const dim3 block(NW * 64);
     // Keep-bit words only from the unsplit forward (the training path).
     const bool dmask = !SPLIT && dropout && a.drop_mask != nullptr;
-    // Without dropout or key slices: two query blocks per wave (2 to 3% faster
-    // than the pipelined single block) when that still fills every slot of two
-    // workgroups per CU; otherwise (short query ranges: prefill chunks) one
-    // block per wave, for twice the workgroups.  Dropout keeps one block per
-    // wave, whose keep-bit words hold one query per lane.
-    const bool two = !SPLIT && !dropout &&
+    // Without key slices or keep-bit words: two query blocks per wave (2 to 3%
+    // faster than the pipelined single block) when that still fills every
+    // slot of two workgroups per CU; otherwise (short query ranges: prefill
+    // chunks) one block per wave, for twice the workgroups.  With keep-bit
+    // words the two-block kernel would spill (two words per lane and tile
+    // under construction), so they keep one block per wave.
+    const bool two = !SPLIT && !dmask &&
                      (int64_t)((a.S + qwg_of(2) - 1) / qwg_of(2)) * a.B * a.H >= 2 * (int64_t)device_cus();
     const int nqblk = (a.S + (two ? qwg_of(2) : qwg_of(1)) - 1) / (two ? qwg_of(2) : qwg_of(1));
     const dim3 grid((unsigned)(nqblk * a.B * a.H * (SPLIT ? a.nsplit : 1)));
     if (causal) {
-        if (dmask)
+        if (two) {
+            if (dropout)
+                hipLaunchKernelGGL((fwd_kernel<true, true, false, false, 2>), grid, block, 0, st, a);
+            else
+                hipLaunchKernelGGL((fwd_kernel<true, false, false, false, 2>), grid, block, 0, st, a);
+        } else if (dmask)
             hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, !SPLIT, 1>), grid, block, 0, st, a);
         else if (dropout)
             hipLaunchKernelGGL((fwd_kernel<true, true, SPLIT, false, 1>), grid, block, 0, st, a);
-        else if (two)
-            hipLaunchKernelGGL((fwd_kernel<true, false, false, false, 2>), grid, block, 0, st, a);
         else
             hipLaunchKernelGGL((fwd_kernel<true, false, SPLIT, false, 1>), grid, block, 0, st, a);
     } else {
-        if (dmask)
+        if (two) {
+            if (dropout)
+                hipLaunchKernelGGL((fwd_kernel<false, true, false, false, 2>), grid, block, 0, st, a);
+            else
+                hipLaunchKernelGGL((fwd_kernel<false, false, false, false, 2>), grid, block, 0, st, a);
+        } else if (dmask)
             hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, !SPLIT, 1>), grid, block, 0, st, a);
         else if (dropout)
             hipLaunchKernelGGL((fwd_kernel<false, true, SPLIT, false, 1>), grid, block, 0, st, a);
-        else if (two)
-            hipLaunchKernelGGL((fwd_kernel<false, false, false, false, 2>), grid, block, 0, st, a);
         else
             hipLaunchKernelGGL((fwd_kernel<false, false, SPLIT, false, 1>), grid, block, 0, st, a);
     }
