@@ -133,9 +133,9 @@ int fa2_fwd_kv_split_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_of
  *     the accumulator with fp32 atomics, then dQ = scale * accumulator.
  *     Slower on MI355X (the atomics are L2-throughput bound); kept selectable.
  * The workspace (fa2_bwd_workspace_bytes) holds delta[b,h,i] = sum_d O*dO and
- * LSE[b,h,i] * log2(e) in fp32, the same per-row terms as bf16 parts for the
- * dK/dV step's MFMAs (all written by the dQ or delta step, read by the dK/dV
- * step) and the fp32 dQ accumulator.  B*H*S must be below 2^30. */
+ * LSE[b,h,i] * log2(e) in fp32, the per-row terms -LSE*log2(e)/scale2 and
+ * -delta that start the dK/dV step's accumulators (all written by the dQ or
+ * delta step, read by the dK/dV step) and the fp32 dQ accumulator.  B*H*S must be below 2^30. */
 typedef struct fa2_bwd_params {
     const void *q, *k, *v, *o, *dout;   /* fp16 [B,H,S,64]                     */
     const float *lse;                   /* fp32 [B,H,S] from the forward       */
@@ -159,7 +159,7 @@ typedef struct fa2_bwd_params {
 
 /* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta and scaled LSE
  * (8*B*H*S bytes, rounded up to 256), the row terms -LSE*log2(e)/scale2 and
- * -delta as three bf16 parts each (16*B*H*ceil32(S) bytes, rounded up to 256),
+ * -delta in fp32 (8*B*H*ceil32(S) bytes, rounded up to 256),
  * then the fp32 dQ accumulator (256*B*H*S bytes). */
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S);
 
@@ -174,7 +174,7 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc); the caller still provides inputs and outputs.
  *   - Size limit: fa2_bwd_noalloc_scratch_bytes(B, H, S) (delta, scaled LSE and
- *     the row terms: about 24*B*H*S bytes) must not exceed
+ *     the row terms: about 16*B*H*S bytes) must not exceed
  *     FA2_BWD_SCRATCH_MAX_BYTES, else FA2_ERR_WORKSPACE; the fused backward
  *     (mode bit 8, which needs a 256*B*H*S-byte accumulator) is rejected with
  *     FA2_ERR_BAD_ARGUMENT.

@@ -108,10 +108,10 @@ def test_empty_problem_is_a_noop():
     for dim in ("B", "H", "S"):
         p = _dummy_fwd(**{dim: 0})
         assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 0
-    # fp32 delta and LSE (rounded to 256 B), bf16 row terms (16 B per query, S rounded to 32,
+    # fp32 delta and LSE (rounded to 256 B), fp32 row terms (8 B per query, S rounded to 32,
     # rounded to 256 B), fp32 dQ accumulator
-    assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 256 + 2 * 3 * 32 * 16 + 2 * 3 * 5 * 64 * 4
-    assert lib.fa2_bwd_workspace_bytes(1, 1, 33) == 512 + 1024 + 33 * 64 * 4
+    assert lib.fa2_bwd_workspace_bytes(2, 3, 5) == 256 + 2 * 3 * 32 * 8 + 2 * 3 * 5 * 64 * 4
+    assert lib.fa2_bwd_workspace_bytes(1, 1, 33) == 512 + 512 + 33 * 64 * 4
     assert lib.fa2_bwd_workspace_bytes(0, 3, 5) == 0
 
 
@@ -177,7 +177,7 @@ def test_bwd_noalloc_rejects_before_any_hip_call():
     """The allocation-free backward checks its size limit and mode before touching the
     device (it would otherwise look up its scratch array on the current GPU)."""
     lib = capi.load()
-    assert lib.fa2_bwd_noalloc_scratch_bytes(2, 3, 5) == 256 + 2 * 3 * 32 * 16
+    assert lib.fa2_bwd_noalloc_scratch_bytes(2, 3, 5) == 256 + 2 * 3 * 32 * 8
     assert lib.fa2_bwd_noalloc_scratch_bytes(0, 3, 5) == 0
     p = capi.BwdParams()
     p.B, p.H, p.S, p.D, p.softmax_scale = 64, 64, 4096, 64, 0.125

@@ -29,21 +29,18 @@
 namespace fa2 {
 namespace {
 
-// Word index of query q's 8-byte slot for term `which` (0: -LSE*log2(e)/scale2,
-// 1: -delta) in the workspace's per-row bf16 parts: blocks of 512 bytes per
-// 32 queries of a (b,h), the 32 first terms then the 32 second terms.
-__device__ __forceinline__ int64_t trip_word(int S, int bh, int q, int which) {
+// Word index of query q's term `which` (0: -LSE*log2(e)/scale2, 1: -delta),
+// fp32, in the workspace's per-row terms: blocks of 64 words per 32 queries of
+// a (b,h), the 32 first terms then the 32 second terms -- one 32-query tile's
+// block is one 256-byte transfer.
+__device__ __forceinline__ int64_t row_term_word(int S, int bh, int q, int which) {
     const int nb = (S + 31) >> 5;
-    return ((int64_t)bh * nb + (q >> 5)) * 128 + which * 64 + 2 * (q & 31);
+    return ((int64_t)bh * nb + (q >> 5)) * 64 + which * 32 + (q & 31);
 }
 // Writes both terms of query q (lse2 = LSE * log2(e)).
 __device__ __forceinline__ void store_row_terms(const BwdArgs &a, int bh, int q, float lse2, float delta) {
-    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-    uint32_t w0, w1;
-    split3_words(-lse2 / a.scale2, w0, w1);
-    *reinterpret_cast<u2v *>(a.trip + trip_word(a.S, bh, q, 0)) = u2v{w0, w1};
-    split3_words(-delta, w0, w1);
-    *reinterpret_cast<u2v *>(a.trip + trip_word(a.S, bh, q, 1)) = u2v{w0, w1};
+    a.trip[row_term_word(a.S, bh, q, 0)] = __builtin_bit_cast(uint32_t, -lse2 / a.scale2);
+    a.trip[row_term_word(a.S, bh, q, 1)] = __builtin_bit_cast(uint32_t, -delta);
 }
 
 // ---------------------------------------------------------------------------
@@ -704,6 +701,9 @@ constexpr int KP_KWG = KP_NW * 32;    // keys per workgroup
 #endif
 constexpr int KP_NST = FA2_KV_NST;    // LDS stages: tiles t-1, t, t+1 resident, t+2 .. in flight (4..6)
 static_assert(KP_NST >= 4 && KP_NST <= 6, "dK/dV stages");
+#ifndef FA2_KV_CINIT_CHUNK
+#define FA2_KV_CINIT_CHUNK 2
+#endif
 
 // A workgroup owns 128 keys (32 per wave; K^T and V^T stay in registers) and
 // streams 32-query tiles: Q and dO by direct global->LDS transfers into
@@ -716,11 +716,11 @@ static_assert(KP_NST >= 4 && KP_NST <= 6, "dK/dV stages");
 // quantities per key tile).
 //
 // FOLD (no dropout; the host also requires scale2 >= 1e-20): the row terms
-// -lse2/scale2 and -delta enter the S and dP accumulators through one bf16
-// MFMA step each (their three bf16 parts, written by the dQ or delta pass,
-// against ones), so P = exp2(S*scale2) and dS = P * dP take no per-element
-// row statistics from LDS and no subtraction.  Otherwise the tile's lse2 and
-// delta are read from LDS per element.
+// -lse2/scale2 and -delta (fp32, written by the dQ or delta pass) are the
+// initial values of the S and dP accumulators -- the first MFMA of each chain
+// takes them as its C operand -- so P = exp2(S*scale2) and dS = P * dP take no
+// per-element row statistics and no subtraction.  Otherwise the tile's lse2
+// and delta are read from LDS per element.
 //
 // DMASK (dropout with a.drop_mask): the keep bits come from the words the
 // forward wrote: per 32-query tile, the words of both 64-key tiles of the
@@ -731,10 +731,9 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     static_assert(!(FOLD && DROPOUT), "the folded row terms assume no dropout");
     static_assert(!DMASK || DROPOUT, "keep-bit words only with dropout");
     __shared__ __attribute__((aligned(16))) h8 sQD[KP_NST][2][KP_QT * 8];   // Q, dO tiles (4 KB each)
-    // Per stage: lse2[32], delta[32] (fp32); FOLD: the 512-byte block of bf16
-    // row terms (and a duplicate from the transfer's upper 32 lanes).
-    __shared__ __attribute__((aligned(16))) float sLD[KP_NST][FOLD ? 256 : 2 * KP_QT];
-    __shared__ __attribute__((aligned(16))) uint32_t sZero[2];
+    // Per stage: lse2[32], delta[32] (fp32); FOLD: the row terms -lse2/scale2
+    // and -delta in the same places.
+    __shared__ __attribute__((aligned(16))) float sLD[KP_NST][2 * KP_QT];
     // DMASK: per stage, run s = 2*i + g2' holds the 32 words of 64-key tile
     // 2*kblk + i, half g2' (and a copy from the transfer's upper 32 lanes).
     __shared__ __attribute__((aligned(16))) uint32_t sDM[DMASK ? KP_NST : 1][256];
@@ -785,8 +784,7 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     // (L & 7) ^ swz_both(row) of query row q0 + row (rows past S: row S - 1,
     // masked on use).  Wave 0 also moves the tile's lse2 (lanes 0..31) and
     // delta (lanes 32..63) from the workspace, where lse2 = delta + B*H*S.
-    // FOLD: wave 0's lanes 0..31 move the tile's 512-byte block of row terms
-    // instead (lanes 32..63 repeat it into the stage's upper half).
+    // FOLD: wave 0 moves the tile's 256-byte block of row terms instead.
     const int trow = 8 * wave + (lane >> 3);
     const int tch = (lane & 7) ^ swz_both(trow);
     auto tile_offsets = [&](int q0, uint32_t &qo, uint32_t &doo) FA2_INLINE {
@@ -804,9 +802,9 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     // recomputed with 64-bit multiplies at every transfer.
     uint64_t gq = (uint64_t)(uintptr_t)(Qp + (int64_t)q_start * a.qss);
     uint64_t gdo = (uint64_t)(uintptr_t)(dOp + (int64_t)q_start * a.doss);
-    uint64_t gld = FOLD ? (uint64_t)(uintptr_t)(a.trip + trip_word(S, bh, q_start, 0))
+    uint64_t gld = FOLD ? (uint64_t)(uintptr_t)(a.trip + row_term_word(S, bh, q_start, 0))
                         : (uint64_t)(uintptr_t)(a.delta + (int64_t)bh * S + q_start);
-    const uint32_t ldoff_t = FOLD ? 16u * (uint32_t)(lane & 31) : ldoff;
+    const uint32_t ldoff_t = FOLD ? 4u * (uint32_t)lane : ldoff;
     const uint64_t dq_step = (uint64_t)KP_QT * a.qss * 2, ddo_step = (uint64_t)KP_QT * a.doss * 2;
     int qn = q_start;          // first query of the next tile to issue
     uint32_t stn = 0;          // its stage
@@ -822,18 +820,13 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
         if (qn + KP_QT > S) tile_offsets(qn, qo, doo);
         lds_dma16_at(gq, qo, lds_qd + stn * (uint32_t)sizeof(sQD[0]));
         lds_dma16_at(gdo, doo, lds_qd + stn * (uint32_t)sizeof(sQD[0]) + (uint32_t)sizeof(sQD[0][0]));
-        if (wave == 0) {
-            if (FOLD)
-                lds_dma16_at(gld, ldoff_t, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
-            else
-                lds_dma4_at(gld, ldoff_t, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
-        }
+        if (wave == 0) lds_dma4_at(gld, ldoff_t, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
         if (DMASK && wave == 1)
             lds_dma16_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(bh, S, 2 * kblk, 0, qn)), dmoff,
                          lds_dm + stn * (uint32_t)sizeof(sDM[0]));
         gq += dq_step;
         gdo += ddo_step;
-        gld += FOLD ? 512 : KP_QT * sizeof(float);
+        gld += FOLD ? 2 * KP_QT * sizeof(float) : KP_QT * sizeof(float);
         qn += KP_QT;
         stn = (stn + 1 == KP_NST) ? 0 : stn + 1;
     };
@@ -875,18 +868,18 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
         return tr_read8_both(reinterpret_cast<const _Float16 *>(sQD[stage][which]), toff[db][0], toff[db][1],
                              16 * hh);
     };
-    // FOLD: A operand of the bf16 step adding row term `which` of the tile in
-    // `stage` (lane (c, g2 = 0): the three parts of query row c in k = 0..2;
-    // lanes g2 = 1: zeros), and its B operand, ones in k = 0..2.
-    const b8 ones3 = g2 == 0 ? ones3_b8() : zero_b8();
-    auto aread = [&](int stage, int which) FA2_INLINE {
-        typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-        const char *src = g2 == 0 ? reinterpret_cast<const char *>(sLD[stage]) + 256 * which + 8 * c
-                                  : reinterpret_cast<const char *>(sZero);
-        const u2v w = *reinterpret_cast<const u2v *>(src);
-        const u4v v = {w[0], w[1], 0u, 0u};
-        return __builtin_bit_cast(b8, v);
+    // FOLD: the initial accumulator of the S (which = 0) or dP (which = 1)
+    // chain of the tile in `stage`: element 4i + j holds the row term of query
+    // row 8i + 4*g2 + j (four 16-byte reads, the same for every lane of a half).
+    auto cinit = [&](int stage, int which) FA2_INLINE {
+        f16x v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f4 x = *reinterpret_cast<const f4 *>(&sLD[stage][KP_QT * which + 8 * i + 4 * g2]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[4 * i + j] = x[j];
+        }
+        return v;
     };
 
     // S = Q K^T and dP = dO V^T of the tile in `stage`: rows = the tile's
@@ -901,8 +894,8 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
                 nd = rread(stage, 1, st + 1);
             }
             if (st == 0 && FOLD) {
-                s = mfma32(fq, kf[0], mfma32_bf16_first(aread(stage, 0), ones3));
-                dp = mfma32(fd, vf[0], mfma32_bf16_first(aread(stage, 1), ones3));
+                s = mfma32(fq, kf[0], cinit(stage, 0));
+                dp = mfma32(fd, vf[0], cinit(stage, 1));
             } else if (st == 0) {
                 s = mfma32_first(fq, kf[0]);
                 dp = mfma32_first(fd, vf[0]);
@@ -1008,11 +1001,6 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
         f4 l4[4], d4[4];
         u4v m4[4];
         stats(sc_, l4, d4, m4);
-        b8 al, ad;
-        if (FOLD) {
-            al = aread(sn, 0);
-            ad = aread(sn, 1);
-        }
         // chunk i < 4: dK/dV for (db, hh) = (i >> 1, i & 1); i >= 4: S/dP for d-step i - 4
         h8 n0 = tread(sp, 1, 0, 0), n1 = tread(sp, 0, 0, 0);
 #pragma unroll
@@ -1029,9 +1017,9 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
                 const int db = i >> 1, hh = i & 1;
                 dv[db] = mfma32(f0, pb_p[hh], dv[db]);
                 dk[db] = mfma32(f1, ds_p[hh], dk[db]);
-                if (FOLD && i == 3) {
-                    s_n = mfma32_bf16_first(al, ones3);
-                    dp_n = mfma32_bf16_first(ad, ones3);
+                if (FOLD && i == FA2_KV_CINIT_CHUNK) {
+                    s_n = cinit(sn, 0);
+                    dp_n = cinit(sn, 1);
                 }
             } else if (i == 4 && FOLD) {
                 s_n = mfma32(f0, kf[0], s_n);
@@ -1075,10 +1063,6 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     f16x sA, dpA, sB, dpB;
     h8 pbA[2], dsA[2], pbB[2], dsB[2];
     const int tl = ntiles - 1;
-    if (FOLD && tid == 0) {   // the zero A-operand half of aread (published by the barrier below)
-        sZero[0] = 0u;
-        sZero[1] = 0u;
-    }
     // Initial wait: tiles 0 and 1 landed, tiles 2 .. NST-2 may be in flight.
     wait_tiles(min(KP_NST - 3, ntiles - 2));
     lds_barrier();

@@ -231,14 +231,14 @@ int fa2_fwd_kv_split_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_of
 }
 
 // Workspace: fp32 delta and log2-scaled LSE, [B*H*S] each (rounded up to 256
-// bytes); the per-row bf16 parts of -LSE*log2(e)/scale2 and -delta, 16 bytes
+// bytes); the per-row terms -LSE*log2(e)/scale2 and -delta in fp32, 8 bytes
 // per query with S rounded up to 32 (rounded up to 256 bytes); then the fp32
 // dQ accumulator [B*H*S*64] of the fused backward.
 static size_t delta_bytes(int32_t B, int32_t H, int32_t S) {
     return ((size_t)B * H * S * 2 * sizeof(float) + 255) & ~(size_t)255;
 }
 static size_t terms_bytes(int32_t B, int32_t H, int32_t S) {
-    return ((size_t)B * H * (((size_t)S + 31) & ~(size_t)31) * 16 + 255) & ~(size_t)255;
+    return ((size_t)B * H * (((size_t)S + 31) & ~(size_t)31) * 8 + 255) & ~(size_t)255;
 }
 
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S) {

@@ -39,10 +39,10 @@ struct BwdArgs {
     _Float16 *dq, *dk, *dv;
     float *delta;        // [B*H, S] fp32 workspace: delta = rowsum(dO * O)
     float *lse2;         // [B*H, S] fp32 workspace: LSE * log2(e), right after delta
-    // Per 32-query block of each (b,h) (blocks of 512 bytes, S rounded up to
-    // 32): for each query, -LSE*log2(e)/scale2 then -delta, each as three bf16
-    // parts in 8 bytes (hi | mid << 16, lo) -- the per-row terms the dK/dV
-    // pass adds into its S and dP accumulators with one bf16 MFMA step each.
+    // Per 32-query block of each (b,h) (blocks of 256 bytes, S rounded up to
+    // 32): the block's 32 values of -LSE*log2(e)/scale2, then its 32 values of
+    // -delta, fp32 -- the per-row terms the dK/dV pass starts its S and dP
+    // accumulators from.
     uint32_t *trip;
     float *dqacc;        // [B*H, S, 64] fp32 dQ accumulator of the fused backward (or null)
     int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss;
