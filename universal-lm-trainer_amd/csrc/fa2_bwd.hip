@@ -1142,14 +1142,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         j = L / BH;
         bh = L - j * BH;
     }
-    // j = 0: key block 0, the heaviest under the causal mask, first.
-    dkv_block<CAUSAL, DROPOUT, FOLD, DMASK>(a, j, bh);
-    if (pair && nkb - 1 - j != j) {
+    // Single blocks: j = 0, the heaviest under the causal mask, first.  Pairs:
+    // every other workgroup runs its short block first, so that the
+    // workgroups sharing a CU, which start together and carry equal work, do
+    // not also reach their block change (the next block's first loads, the
+    // previous one's stores) at the same time.
+    const bool swap = pair && ((L >> 3) & 1);
+    const int ja = swap ? nkb - 1 - j : j, jb = swap ? j : nkb - 1 - j;
+    dkv_block<CAUSAL, DROPOUT, FOLD, DMASK>(a, ja, bh);
+    if (pair && jb != ja) {
         // The first block's dK/dV staging reads must finish before the second
         // block's transfers land in the same LDS.  (Two inlined copies of the
         // block: a loop over both keeps values live across them and spills.)
         lds_barrier();
-        dkv_block<CAUSAL, DROPOUT, FOLD, DMASK>(a, nkb - 1 - j, bh);
+        dkv_block<CAUSAL, DROPOUT, FOLD, DMASK>(a, jb, bh);
     }
 }
 
