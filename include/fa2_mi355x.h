@@ -59,7 +59,8 @@ typedef struct fa2_fwd_params {
     int32_t causal;                 /* nonzero: key j visible to query i iff j <= i */
     uint32_t *dropout_mask;         /* optional keep-bit output, see below; NULL = none */
     size_t dropout_mask_bytes;      /* bytes at dropout_mask: with dropout_p > 0 at least
-                                       fa2_dropout_mask_bytes(B, H, S), else
+                                       fa2_dropout_mask_bytes_causal(B, H, S) when causal,
+                                       fa2_dropout_mask_bytes(B, H, S) otherwise, else
                                        FA2_ERR_WORKSPACE (ignored when dropout_mask is NULL) */
 } fa2_fwd_params;
 
@@ -68,8 +69,10 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
 /* Dropout keep bits.  With dropout_p > 0 and dropout_mask non-NULL,
  * fa2_fwd_f16 also stores the keep bit of every (query, key) pair it computes
  * -- the same bits its dropout hash draws -- into dropout_mask
- * (fa2_dropout_mask_bytes(B, H, S) bytes, 16-byte aligned; words it does not
- * compute, such as those above the causal diagonal, are left as they were).
+ * (fa2_dropout_mask_bytes_causal(B, H, S) bytes with the causal mask,
+ * fa2_dropout_mask_bytes(B, H, S) without, 16-byte aligned; words it does not
+ * compute, such as those of queries a key tile only partly reaches, are left
+ * as they were).
  * fa2_bwd_f16 given the same words in its dropout_mask (with the same B, H,
  * S, causal, dropout_p and seed) reads them instead of hashing again: the
  * results are identical, the backward's hash work is gone, and the words cost
@@ -77,11 +80,19 @@ int fa2_fwd_f16(const fa2_fwd_params *p, void *stream);
  * The fa2_fwd_kv_* entry points take no mask (dropout_mask must be NULL).
  * No counterpart in the reference, which draws its dropout with curand in
  * the forward only (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:40-364).
- * Word layout, per (b, h), 64-key tile t (< 2*ceil(S/128)), half g (0, 1) and
- * query i (< R = S rounded up to 256): word ((b*H + h)*T + t)*2*R + g*R + i,
- * T = 2*ceil(S/128); its bit 31 - (16*kb + 8*hh + e) is key
- * 64*t + 32*kb + 16*hh + 8*(e/4) + 4*g + e%4 (kb, hh in 0..1, e in 0..7). */
+ * Word layout, per (b, h), 64-key tile t (< T = 2*ceil(S/128)), half g (0, 1)
+ * and query i (< R = S rounded up to 256); the word's bit
+ * 31 - (16*kb + 8*hh + e) is key 64*t + 32*kb + 16*hh + 8*(e/4) + 4*g + e%4
+ * (kb, hh in 0..1, e in 0..7).
+ *   - Without the causal mask: word ((b*H + h)*T + t)*2*R + g*R + i.
+ *   - With it, tile t keeps queries i >= r = 128*(t/2) only (earlier queries
+ *     see none of its keys), in runs of n = R - r words: word
+ *     (b*H + h)*W(T/2) + W(t/2) + (t%2)*2*n + g*n + (i - r), where
+ *     W(j) = 4*j*R - 256*j*(j-1) counts the words of the tiles before 2*j.
+ *     That is about half of the square layout's bytes. */
 size_t fa2_dropout_mask_bytes(int32_t B, int32_t H, int32_t S);
+/* Bytes of the keep-bit words of a causal call: B*H*W(T/2)*4 (see above). */
+size_t fa2_dropout_mask_bytes_causal(int32_t B, int32_t H, int32_t S);
 
 /* The integer form of the reference's keep test, which every kernel uses:
  * (h >> 8) * 2^-24 >= p in fp32 (exact, since h >> 8 < 2^24) holds iff

@@ -30,18 +30,32 @@ def rand_inputs(B, H, S, seed):
     return [torch.randn(B, H, S, 64, generator=g).half().to(DEV) for _ in range(4)]
 
 
-def mask_bits(words, B, H, S):
-    """[B*H, S, S] keep bits (query row, key col) read out of the words: word
-    ((bh*T + t)*2 + g)*R + i, bit 31 - (16*kb + 8*hh + e) holds key
-    64*t + 32*kb + 16*hh + 8*(e//4) + 4*g + e%4 (T = 2*ceil(S/128), R = S rounded up to 256)."""
+def mask_bits(words, B, H, S, causal=False):
+    """[B*H, S, S] keep bits (query row, key col) read out of the words through the
+    layout include/fa2_mi355x.h documents: bit 31 - (16*kb + 8*hh + e) of the word of
+    (tile t, half g, query i) holds key 64*t + 32*kb + 16*hh + 8*(e//4) + 4*g + e%4
+    (T = 2*ceil(S/128) tiles, R = S rounded up to 256 queries).  Without the causal mask the
+    word is ((bh*T + t)*2 + g)*R + i; with it, tile t keeps queries i >= r = 128*(t//2) in
+    runs of n = R - r words, word bh*W(T/2) + W(t//2) + (t%2)*2*n + g*n + (i - r), with
+    W(j) = 4*j*R - 256*j*(j-1).  Pairs a causal layout does not hold read as False."""
     T, R = 2 * ((S + 127) // 128), (S + 255) // 256 * 256
-    w = words.reshape(B * H, T, 2, R)[:, :, :, :S]
-    j = np.arange(S)
-    t, r = j // 64, j % 64
+    key = np.arange(S)
+    t, r = key // 64, key % 64
     kb, hh, e_hi, g, e_lo = r // 32, (r // 16) % 2, (r // 8) % 2, (r // 4) % 2, r % 4
     bit = 31 - (16 * kb + 8 * hh + 4 * e_hi + e_lo)
-    sel = w[:, t, g, :]                                  # [BH, S keys, S rows]
-    return ((sel >> bit[None, :, None].astype(np.uint32)) & 1).transpose(0, 2, 1).astype(bool)
+    row = np.arange(S)[:, None]                          # [S rows, 1]
+    if causal:
+        W = lambda j: 4 * j * R - 256 * j * (j - 1)
+        j, o = t // 2, t % 2
+        r0, n = 128 * j, R - 128 * j
+        held = row >= r0[None, :]                        # [S rows, S keys]
+        idx = np.where(held, W(j) + o * 2 * n + g * n + (row - r0), 0)
+        w = words.reshape(B * H, W(T // 2))[:, idx]      # [BH, S rows, S keys]
+    else:
+        held = np.ones((S, S), bool)
+        w = words.reshape(B * H, T * 2 * R)[:, ((t * 2 + g) * R)[None, :] + row]
+    bits = ((w >> bit[None, None, :].astype(np.uint32)) & 1).astype(bool)
+    return bits & held[None]
 
 
 SHAPES = [(1, 2, 1), (1, 2, 63), (2, 2, 160), (1, 3, 257), (1, 1, 513), (2, 2, 1000)]
@@ -57,7 +71,9 @@ def test_mask_path_bitwise_equals_hash_path(fa, B, H, S, causal, p):
     seed = 0x5EED + S
     o, lse = ext.fa_fwd(q, k, v, p, causal, 0.125, seed)
     o2, lse2, mask = ext.fa_fwd_mask(q, k, v, p, causal, 0.125, seed)
-    assert mask.dtype == torch.int32 and mask.numel() * 4 == capi.load().fa2_dropout_mask_bytes(B, H, S)
+    lib = capi.load()
+    want_bytes = lib.fa2_dropout_mask_bytes_causal(B, H, S) if causal else lib.fa2_dropout_mask_bytes(B, H, S)
+    assert mask.dtype == torch.int32 and mask.numel() * 4 == want_bytes
     assert torch.equal(o, o2) and torch.equal(lse, lse2)
     ref = ext.fa_bwd(q, k, v, o, lse, do, p, causal, 0.125, seed, 7)
     got = ext.fa_bwd(q, k, v, o, lse, do, p, causal, 0.125, seed, 7, mask=mask)
@@ -85,11 +101,12 @@ def test_mask_words_match_oracle_keep(fa, causal, S):
     lib = capi.load()
     o = torch.empty_like(q)
     lse = torch.empty(B, H, S, device=DEV)
-    words = torch.full((lib.fa2_dropout_mask_bytes(B, H, S) // 4,), 0x55555555, dtype=torch.int32, device=DEV)
+    nbytes = lib.fa2_dropout_mask_bytes_causal(B, H, S) if causal else lib.fa2_dropout_mask_bytes(B, H, S)
+    words = torch.full((nbytes // 4,), 0x55555555, dtype=torch.int32, device=DEV)
     prm = capi.fwd_params(q, k, v, o, lse, 0.125, causal=causal, dropout_p=p, seed=seed, mask=words)
     assert lib.fa2_fwd_f16(ctypes.byref(prm), None) == 0, lib.fa2_last_error()
     torch.cuda.synchronize()
-    got = mask_bits(words.cpu().numpy().view(np.uint32), B, H, S)
+    got = mask_bits(words.cpu().numpy().view(np.uint32), B, H, S, causal)
     want = orc.keep_mask(seed, B, H, S, p).reshape(B * H, S, S)
     vis = np.ones((S, S), bool) if not causal else np.tri(S, dtype=bool)
     bad = (got != want) & vis[None]

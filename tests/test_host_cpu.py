@@ -124,6 +124,11 @@ def test_dropout_mask_size_and_validation():
     assert lib.fa2_dropout_mask_bytes(8, 12, 4096) == 96 * 64 * 2 * 4096 * 4
     assert lib.fa2_dropout_mask_bytes(2, 3, 257) == 6 * 6 * 2 * 512 * 4
     assert lib.fa2_dropout_mask_bytes(0, 3, 5) == 0 and lib.fa2_dropout_mask_bytes(1, 1, -1) == 0
+    # causal: 128-key block j keeps 4 runs (2 tiles x 2 halves) of R - 128 j words
+    assert lib.fa2_dropout_mask_bytes_causal(1, 1, 1) == 4 * 256 * 4
+    assert lib.fa2_dropout_mask_bytes_causal(2, 3, 257) == 6 * 4 * (512 + 384 + 256) * 4
+    assert lib.fa2_dropout_mask_bytes_causal(8, 12, 4096) == 96 * 4 * sum(4096 - 128 * j for j in range(32)) * 4
+    assert lib.fa2_dropout_mask_bytes_causal(0, 3, 5) == 0
     p = _dummy_fwd(dropout_p=0.1, dropout_mask=(1 << 21) + 4)
     assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 3, lib.fa2_last_error()
     assert b"dropout_mask" in lib.fa2_last_error()
@@ -143,7 +148,7 @@ def test_dropout_mask_size_and_validation():
     assert b"dropout_mask" in lib.fa2_last_error()
     # An undersized mask buffer (the device writes would run past it) is rejected before any
     # launch, in the forward and the backward; its size only matters when dropout uses it.
-    fwd_need = lib.fa2_dropout_mask_bytes(2, 8, 16)
+    fwd_need = lib.fa2_dropout_mask_bytes_causal(2, 8, 16)   # _dummy_fwd is causal
     p = _dummy_fwd(dropout_p=0.1, dropout_mask=1 << 21, dropout_mask_bytes=fwd_need - 4)
     assert lib.fa2_fwd_f16(ctypes.byref(p), None) == 5, lib.fa2_last_error()
     assert b"dropout_mask needs" in lib.fa2_last_error()
@@ -332,6 +337,7 @@ def test_python_mask_size_matches_c_abi(monkeypatch):
     lib = capi.load()
     for B, H, S in ((1, 1, 1), (2, 3, 257), (8, 12, 4096), (1, 2, 16384), (3, 5, 1000)):
         assert fa.dropout_mask_bytes(B, H, S) == lib.fa2_dropout_mask_bytes(B, H, S), (B, H, S)
+        assert fa.dropout_mask_bytes(B, H, S, causal=True) == lib.fa2_dropout_mask_bytes_causal(B, H, S), (B, H, S)
     monkeypatch.setenv("FA_V100_DROPOUT_MASK_MAX_BYTES", "lots")
     assert fa._mask_cap() == 1 << 30
     monkeypatch.setenv("FA_V100_DROPOUT_MASK_MAX_BYTES", "0")

@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         if (DMASK) {
 #pragma unroll
             for (int half = 0; half < 2; ++half)
-                lds_dma4_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(bh, S, kn / DQ_KT, half, qw0)),
+                lds_dma4_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(CAUSAL, bh, S, kn / DQ_KT, half, qw0)),
                             4u * (uint32_t)lane, lds_mq + stn * (uint32_t)sizeof(sMQ[0]) + 256u * (uint32_t)half);
         }
         gk += k_step;
@@ -811,9 +811,9 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     const uint32_t lds_qd = lds_addr(&sQD[0][0][0]) + 1024u * (uint32_t)wave, lds_ld = lds_addr(&sLD[0][0]);
     // DMASK: lane L of wave 1's transfer moves words 4*(L & 7) .. +3 of run
     // s = (L & 31) >> 3, i.e. of 64-key tile 2*kblk + (s >> 1), half s & 1,
-    // at word s * dmask_rows(S) past the tile's first run (lanes 32..63
-    // repeat lanes 0..31).
-    const uint32_t dmoff = 4u * (uint32_t)(((lane & 31) >> 3) * dmask_rows(S) + 4 * (lane & 7));
+    // at word s * dmask_run(...) past the tile's first run (both tiles of the
+    // block have runs of one length; lanes 32..63 repeat lanes 0..31).
+    const uint32_t dmoff = 4u * (uint32_t)(((lane & 31) >> 3) * dmask_run(CAUSAL, S, 2 * kblk) + 4 * (lane & 7));
     const uint32_t lds_dm = lds_addr(&sDM[0][0]);
     auto issue = [&](int) FA2_INLINE {
         uint32_t qo = qoff0, doo = dooff0;
@@ -822,7 +822,7 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
         lds_dma16_at(gdo, doo, lds_qd + stn * (uint32_t)sizeof(sQD[0]) + (uint32_t)sizeof(sQD[0][0]));
         if (wave == 0) lds_dma4_at(gld, ldoff_t, lds_ld + stn * (uint32_t)sizeof(sLD[0]));
         if (DMASK && wave == 1)
-            lds_dma16_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(bh, S, 2 * kblk, 0, qn)), dmoff,
+            lds_dma16_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(CAUSAL, bh, S, 2 * kblk, 0, qn)), dmoff,
                          lds_dm + stn * (uint32_t)sizeof(sDM[0]));
         gq += dq_step;
         gdo += ddo_step;

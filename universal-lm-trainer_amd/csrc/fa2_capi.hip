@@ -72,10 +72,10 @@ float scale2_of(float scale) {
 
 // The keep-bit words are moved in 16-byte transfers and cover every (b, h)
 // at fixed offsets; without dropout they are not touched.
-int check_mask(const void *mask, size_t bytes, int32_t B, int32_t H, int32_t S, float p) {
+int check_mask(const void *mask, size_t bytes, int32_t B, int32_t H, int32_t S, float p, int32_t causal) {
     if (!mask || !(p > 0.f)) return FA2_OK;
     if (reinterpret_cast<uintptr_t>(mask) & 15u) return fail(FA2_ERR_MISALIGNED, "dropout_mask is not 16-byte aligned");
-    const size_t need = fa2_dropout_mask_bytes(B, H, S);
+    const size_t need = causal ? fa2_dropout_mask_bytes_causal(B, H, S) : fa2_dropout_mask_bytes(B, H, S);
     if (bytes < need) return fail(FA2_ERR_WORKSPACE, "dropout_mask needs %zu bytes, got %zu", need, bytes);
     return FA2_OK;
 }
@@ -133,6 +133,13 @@ size_t fa2_dropout_mask_bytes(int32_t B, int32_t H, int32_t S) {
     return (size_t)B * H * tiles * 2 * rows * sizeof(uint32_t);
 }
 
+// Causal: 128-key block j keeps runs of R - 128 j words (4 runs: 2 tiles x 2 halves).
+size_t fa2_dropout_mask_bytes_causal(int32_t B, int32_t H, int32_t S) {
+    if (B <= 0 || H <= 0 || S <= 0) return 0;
+    const size_t J = ((size_t)S + 127) / 128, R = ((size_t)S + 255) & ~(size_t)255;
+    return (size_t)B * H * (4 * J * R - 256 * J * (J - 1)) * sizeof(uint32_t);
+}
+
 size_t fa2_fwd_kv_workspace_bytes(int32_t B, int32_t H, int32_t S, int32_t nsplit) {
     if (B <= 0 || H <= 0 || S <= 0 || nsplit <= 1) return 0;
     return kv_part_bytes(B, H, S, nsplit);
@@ -178,7 +185,7 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
     if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
     if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
-    if ((rc = check_mask(p->dropout_mask, p->dropout_mask_bytes, p->B, p->H, p->S, p->dropout_p))) return rc;
+    if ((rc = check_mask(p->dropout_mask, p->dropout_mask_bytes, p->B, p->H, p->S, p->dropout_p, p->causal))) return rc;
 
     fa2::FwdArgs a;
     a.q = static_cast<const _Float16 *>(p->q);
@@ -276,7 +283,7 @@ static int bwd_run(const fa2_bwd_params *p, int32_t mode, void *workspace, void 
         if (!p->lse) return fail(FA2_ERR_NULL_POINTER, "lse is NULL");
         if (reinterpret_cast<uintptr_t>(p->lse) & 3u) return fail(FA2_ERR_MISALIGNED, "lse is not 4-byte aligned");
         if (p->lse_stride[0] < 0 || p->lse_stride[1] < 0) return fail(FA2_ERR_BAD_SHAPE, "negative lse stride");
-        if ((rc = check_mask(p->dropout_mask, p->dropout_mask_bytes, p->B, p->H, p->S, p->dropout_p))) return rc;
+        if ((rc = check_mask(p->dropout_mask, p->dropout_mask_bytes, p->B, p->H, p->S, p->dropout_p, p->causal))) return rc;
     }
     struct Out { const char *name; void *ptr; const int64_t *st; };
     const Out outs[3] = {{"dq", p->dq, p->dq_stride}, {"dk", p->dk, p->dk_stride}, {"dv", p->dv, p->dv_stride}};

@@ -419,14 +419,26 @@ __device__ __forceinline__ float keep_multiplier(uint32_t w, int bit, float inv_
 // 64-key tile t64, half g2, query q) at word index dmask_word(...): keys in
 // tiles of 64 with dmask_tiles(S) = 2 * ceil(S / 128) tiles (the dK/dV pass
 // reads both 64-key tiles of its 128-key block), queries padded to
-// dmask_rows(S) = S rounded up to 256 (whole query blocks of every pass).
+// dmask_rows(S) = R = S rounded up to 256 (whole query blocks of every pass).
+// Without the causal mask a run of R words per (tile, half); with it, tile
+// t64 keeps only queries from rb = 128 * (t64 / 2) on -- the first query of
+// its 128-key block, from where the dK/dV pass reads; every earlier query
+// sees none of its keys -- in runs of R - rb words: about half the bytes.
 // Bit 31 - (16*kb + 8*hh + e) of word g2 is key 64*t64 + 32*kb + 16*hh +
 // 8*(e>>2) + 4*g2 + (e&3): the forward's own register order, shifted into
 // the word element by element, so each lane builds one word per tile.
 __device__ __forceinline__ int dmask_tiles(int S) { return 2 * ((S + 127) / 128); }
 __device__ __forceinline__ int dmask_rows(int S) { return (S + 255) & ~255; }
-__device__ __forceinline__ int64_t dmask_word(int bh, int S, int t64, int g2, int q) {
-    return ((int64_t)bh * dmask_tiles(S) + t64) * 2 * dmask_rows(S) + (int64_t)g2 * dmask_rows(S) + q;
+// Words of one (tile, half) run: queries dmask_row0 .. R-1.
+__device__ __forceinline__ int dmask_row0(bool causal, int t64) { return causal ? 128 * (t64 >> 1) : 0; }
+__device__ __forceinline__ int dmask_run(bool causal, int S, int t64) { return dmask_rows(S) - dmask_row0(causal, t64); }
+__device__ __forceinline__ int64_t dmask_word(bool causal, int bh, int S, int t64, int g2, int q) {
+    const int64_t R = dmask_rows(S);
+    if (!causal) return ((int64_t)bh * dmask_tiles(S) + t64) * 2 * R + (int64_t)g2 * R + q;
+    // Blocks j < t64 / 2 hold 4 runs each of R - 128 j words.
+    const int64_t J = dmask_tiles(S) >> 1, j = t64 >> 1, n = R - 128 * j;
+    const int64_t head = 4 * J * R - 256 * J * (J - 1), before = 4 * j * R - 256 * j * (j - 1);
+    return (int64_t)bh * head + before + (int64_t)(t64 & 1) * 2 * n + (int64_t)g2 * n + (q - 128 * j);
 }
 
 }  // namespace fa2

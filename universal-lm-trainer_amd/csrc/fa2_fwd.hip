@@ -503,7 +503,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
                     const int q = qw0 + 32 * qb + c;
-                    if (q < S) a.drop_mask[dmask_word(bh, S, kbase / KT + t, g2, q)] = wq[qb];
+                    if (q < S) a.drop_mask[dmask_word(CAUSAL, bh, S, kbase / KT + t, g2, q)] = wq[qb];
                 }
             }
         }
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         if (t + NST - 1 < ntiles) issue(t + NST - 1);
         if (DMASK && t <= tlast) {
             const int q = qw0 + c;   // QB == 1
-            if (q < S) a.drop_mask[dmask_word(bh, S, kbase / KT + t, g2, q)] = wpend;
+            if (q < S) a.drop_mask[dmask_word(CAUSAL, bh, S, kbase / KT + t, g2, q)] = wpend;
         }
     };
     // Steady state (1 <= t < tsteady): no masking -- the tile is below this

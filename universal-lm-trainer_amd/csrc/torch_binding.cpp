@@ -4,7 +4,7 @@
 // output conventions (reference @ None: csrc/flash_attn_v100/flash_attn_v100.cu:386-397):
 //   fa_fwd(q, k, v, dropout_p, causal, softmax_scale, seed)            -> [o, lse]
 // plus fa_fwd_mask (same arguments) -> [o, lse, mask]: with dropout also the
-// keep-bit words (int32, fa2_dropout_mask_bytes), for fa_bwd(..., mask=)
+// keep-bit words (int32, fa2_dropout_mask_bytes[_causal]), for fa_bwd(..., mask=)
 // to read instead of hashing again (identical gradients);
 // plus, for inference callers (no reference counterpart; fa2_fwd_kv_f16):
 //   fa_fwd_kv(q, k, v, causal, softmax_scale, causal_offset, nsplit=0)  -> [o, lse]
@@ -106,7 +106,9 @@ std::vector<torch::Tensor> fwd_impl(const torch::Tensor &q, const torch::Tensor 
     TORCH_CHECK(k.size(2) <= INT32_MAX && causal_offset >= INT32_MIN && causal_offset <= INT32_MAX,
                 op, ": key length / causal offset out of range");
     if (want_mask) {   // square forward (fa2_fwd_f16), which alone writes keep bits (none without dropout)
-        auto mask = torch::empty({dropout_p > 0.0 ? (int64_t)(fa2_dropout_mask_bytes(p.B, p.H, p.S) / 4) : 0},
+        const size_t mask_bytes = causal ? fa2_dropout_mask_bytes_causal(p.B, p.H, p.S)
+                                         : fa2_dropout_mask_bytes(p.B, p.H, p.S);
+        auto mask = torch::empty({dropout_p > 0.0 ? (int64_t)(mask_bytes / 4) : 0},
                                  q.options().dtype(torch::kInt));
         p.dropout_mask = dropout_p > 0.0 ? reinterpret_cast<uint32_t *>(mask.data_ptr()) : nullptr;
         p.dropout_mask_bytes = (size_t)mask.numel() * 4;
@@ -188,9 +190,10 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
         TORCH_CHECK(mask->is_cuda() && mask->device() == q.device() && mask->dtype() == torch::kInt &&
                         mask->is_contiguous(),
                     "fa_bwd: mask must be the contiguous int32 words fa_fwd_mask returned");
+        const int32_t B = (int32_t)q.size(0), H = (int32_t)q.size(1), S = (int32_t)q.size(2);
         TORCH_CHECK((size_t)mask->numel() * 4 ==
-                        fa2_dropout_mask_bytes((int32_t)q.size(0), (int32_t)q.size(1), (int32_t)q.size(2)),
-                    "fa_bwd: mask size does not match (B, H, S)");
+                        (causal ? fa2_dropout_mask_bytes_causal(B, H, S) : fa2_dropout_mask_bytes(B, H, S)),
+                    "fa_bwd: mask size does not match (B, H, S, causal)");
     }
     at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     // The kernels take any (b,h,s) strides; only rows must be contiguous and

@@ -83,6 +83,8 @@ def load():
         lib.fa2_fwd_kv_workspace_bytes.restype = ctypes.c_size_t
         lib.fa2_dropout_mask_bytes.argtypes = [ctypes.c_int32] * 3
         lib.fa2_dropout_mask_bytes.restype = ctypes.c_size_t
+        lib.fa2_dropout_mask_bytes_causal.argtypes = [ctypes.c_int32] * 3
+        lib.fa2_dropout_mask_bytes_causal.restype = ctypes.c_size_t
         lib.fa2_dropout_threshold.argtypes = [ctypes.c_float]
         lib.fa2_dropout_threshold.restype = ctypes.c_uint32
         lib.fa2_bwd_f16.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int32, ctypes.c_void_p,

@@ -58,8 +58,8 @@ _BUILD_ERROR = None
 _SEED_COUNTER = itertools.count(1)
 
 # Keep-bit words: with dropout, and only when a gradient of q, k or v will be
-# computed, the forward also stores its keep bits (one bit per query/key pair
-# of the square, 201 MB at B=8 H=12 S=4096), saved with the other tensors until
+# computed, the forward also stores its keep bits (one bit per query/key pair,
+# causal: 104 MB at B=8 H=12 S=4096, 201 MB without the mask), saved with the other tensors until
 # the backward, which then reads them instead of hashing again: identical
 # gradients, less backward work.  The words live as long as the autograd graph
 # holds them, i.e. one set per attention call awaiting its backward (ten for a
@@ -77,9 +77,12 @@ def _mask_cap(default=1 << 30):
 DROPOUT_MASK_MAX_BYTES = _mask_cap()
 
 
-def dropout_mask_bytes(B, H, S):
-    """Bytes of the keep-bit words of a (B, H, S) call (fa2_dropout_mask_bytes)."""
-    return B * H * (2 * ((S + 127) // 128)) * 2 * ((S + 255) // 256 * 256) * 4
+def dropout_mask_bytes(B, H, S, causal=False):
+    """Bytes of the keep-bit words of a (B, H, S) call (fa2_dropout_mask_bytes,
+    or fa2_dropout_mask_bytes_causal with the causal mask)."""
+    J, R = (S + 127) // 128, (S + 255) // 256 * 256
+    words = 4 * J * R - 256 * J * (J - 1) if causal else 4 * J * R
+    return B * H * words * 4
 
 
 def _next_seed():
@@ -139,7 +142,7 @@ class _FlashAttnV100Cuda(torch.autograd.Function):
         seed = _next_seed()
         mask = None
         if (dropout_p > 0 and any(ctx.needs_input_grad[:3])
-                and dropout_mask_bytes(*q.shape[:3]) <= DROPOUT_MASK_MAX_BYTES):
+                and dropout_mask_bytes(*q.shape[:3], causal=bool(causal)) <= DROPOUT_MASK_MAX_BYTES):
             o, lse, mask = ext.fa_fwd_mask(q, k, v, float(dropout_p), bool(causal), float(softmax_scale), int(seed))
         else:
             o, lse = ext.fa_fwd(q, k, v, float(dropout_p), bool(causal), float(softmax_scale), int(seed))
