@@ -253,16 +253,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         dq[qb][0] = zero16();
         dq[qb][1] = zero16();
     }
-    // Without dropout, dP^T - delta comes out of the MFMA chain: one extra
-    // bf16 step adds ones(k) * (-delta split into three bf16 parts, exact to
-    // fp32 rounding) over k = 0..2, so dS = P * acc needs no subtraction.
-    // Lanes of k half 1 (g2 = 1) hold zeros in both operands.
-    b8 dmb[DQ_QB], ones3;
-    if (!DROPOUT) {
-#pragma unroll
-        for (int qb = 0; qb < DQ_QB; ++qb) dmb[qb] = g2 == 0 ? split3_bf16(-dl[qb]) : zero_b8();
-        ones3 = g2 == 0 ? ones3_b8() : zero_b8();
-    }
+    // Without dropout, dP^T - delta comes out of the MFMA chain: the dP
+    // accumulator starts at -delta (the lane's query: the same value in all
+    // 16 elements, 16 moves), so dS = P * acc needs no subtraction.  (An
+    // extra bf16 MFMA step adding -delta from three bf16 parts costs 2% more
+    // time in this pass, and 16 subtractions per block 2%.)
 
     // LDS read offsets: K / V rows 32*kb + c at logical chunk 2*st + g2, and
     // K^T through transposing reads (d block db, row half hi).
@@ -350,8 +345,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
                     if (!DROPOUT) {
-                        dpA = mfma32_bf16_first(ones3, dmb[0]);
-                        dpB = mfma32_bf16_first(ones3, dmb[1]);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            dpA[r] = -dl[0];
+                            dpB[r] = -dl[1];
+                        }
                     }
 #pragma unroll
                     for (int sti = 0; sti < 4; ++sti) {

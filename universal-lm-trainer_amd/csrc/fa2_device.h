@@ -71,56 +71,6 @@ __device__ __forceinline__ h8 zero_h8() {
     return z;
 }
 
-// bf16 operands of a 32x32x16 MFMA step that adds a per-column constant to an
-// accumulator (k = 0..2 carry the three parts, the rest are zero).
-typedef __bf16 b8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f16x mfma32_bf16_first(b8 a, b8 b) {
-    const f16x z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, z, 0, 0, 0);
-}
-
-__device__ __forceinline__ b8 zero_b8() {
-    b8 z;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) z[i] = (__bf16)0.f;
-    return z;
-}
-
-__device__ __forceinline__ b8 ones3_b8() {
-    b8 z = zero_b8();
-    z[0] = z[1] = z[2] = (__bf16)1.f;
-    return z;
-}
-
-// x as hi + mid + lo, each a bf16 (8 significant bits) holding what the
-// previous parts leave; each residual is exact in fp32, so the parts sum to x
-// within about 2^-24 |x| (bf16 keeps fp32's exponent range: no underflow).
-__device__ __forceinline__ b8 split3_bf16(float x) {
-    b8 z = zero_b8();
-    const __bf16 hi = (__bf16)x;
-    const float r1 = x - (float)hi;
-    const __bf16 mid = (__bf16)r1;
-    const __bf16 lo = (__bf16)(r1 - (float)mid);
-    z[0] = hi;
-    z[1] = mid;
-    z[2] = lo;
-    return z;
-}
-
-// The same three parts packed into 8 bytes (hi | mid << 16, lo), the form the
-// backward's workspace keeps them in.  A non-finite x keeps hi = x and zero
-// residuals (no inf - inf).
-__device__ __forceinline__ void split3_words(float x, uint32_t &w0, uint32_t &w1) {
-    const bool fin = __builtin_isfinite(x);
-    b8 z = split3_bf16(fin ? x : 0.f);
-    if (!fin) z[0] = (__bf16)x;
-    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-    const u4v w = __builtin_bit_cast(u4v, z);
-    w0 = w[0];
-    w1 = w[1];
-}
-
 // Transposing operand read (ds_read_b64_tr_b16).  From a row-major LDS tile
 // M[k][n] (row stride LD halves), lane 32*g2 + c receives
 //     M[k0 + 8*a + 4*g2 + j][n0 + c]   in slot e = 4*a + j  (a = 0..1, j = 0..3),
