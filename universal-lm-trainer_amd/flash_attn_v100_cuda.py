@@ -53,15 +53,17 @@ _EXT = None
 _BUILD_ERROR = None
 
 # The backward must reuse the forward's dropout mask.  The mask is a pure
-# function of (seed, row, col, bh), so the seed alone (saved in ctx) lets the
-# backward hash it again.
+# function of (seed, row, col, bh), so the seed (saved in ctx) is enough for
+# the backward to hash it again; the keep-bit words below only spare it that
+# work.
 _SEED_COUNTER = itertools.count(1)
 
 # Keep-bit words: with dropout, and only when a gradient of q, k or v will be
-# computed, the forward also stores its keep bits (one bit per query/key pair,
-# causal: 104 MB at B=8 H=12 S=4096, 201 MB without the mask), saved with the other tensors until
-# the backward, which then reads them instead of hashing again: identical
-# gradients, less backward work.  The words live as long as the autograd graph
+# computed, the forward also stores its keep bits (one bit per query/key pair
+# it computes: 104 MB at B=8 H=12 S=4096 causal, 201 MB without the causal
+# mask), saved with the other tensors until the backward, which then reads
+# them instead of hashing again: identical gradients, less backward work.
+# The words live as long as the autograd graph
 # holds them, i.e. one set per attention call awaiting its backward (ten for a
 # ten-layer model).  This cap applies to each call's words on their own, not to
 # their total: a call whose words would exceed it hashes in the backward
