@@ -157,6 +157,30 @@ def clock_over_steps(torch, step, ms_per_step, n=10):
     return out
 
 
+def step_roofline(B, H, S, step_flops, value):
+    """The whole step against its own roofline, attainable = min(MFMA peak,
+    intensity x HBM bandwidth), on two byte counts:
+      * the operation's minimum (any fwd + bwd must move): Q, K, V read and O,
+        LSE written by the forward; Q, K, V, O, dO, LSE read and dQ, dK, dV
+        written by the backward = 12 fp16 tensors of B*H*S*64 + 2 fp32 rows;
+      * this design's (split backward): the forward as above, the dQ pass
+        also writing delta, the scaled LSE and the 8-byte row terms, the
+        dK/dV pass reading Q, K, V, dO and the row terms again = 16 tensors
+        + 8 rows.
+    Short sequences are HBM-bound by either measure."""
+    tensor, row = B * H * S * 64 * 2, B * H * S * 4
+    out = {}
+    for name, nbytes in (("minimum", 12 * tensor + 2 * row), ("split_design", 16 * tensor + 8 * row)):
+        ai = step_flops / nbytes
+        hbm_tflops = ai * HBM_GBS * 1e9 / 1e12
+        attainable = min(PEAK_TFLOPS, hbm_tflops)
+        out[name] = {"bound": "hbm" if hbm_tflops < PEAK_TFLOPS else "mfma", "attainable": round(attainable, 1),
+                     "frac": round(value / attainable, 4), "algorithmic_bytes": nbytes,
+                     "intensity_flop_per_byte": round(ai, 1)}
+    out["unit"] = "TFLOP/s"
+    return out
+
+
 def cpu_baseline():
     """The reference's CPU path (train.py:1956-1961): SDPA fwd + .backward(dO)
     in fp32, timed with the default CPU dispatch (what the reference runs) and
@@ -631,6 +655,7 @@ def main():
                    "bwd_mode": args.bwd_mode},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": round(PEAK_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(dom)},
+        "step_roofline": step_roofline(B, H, S, step_flops, value),
         "kernels": kernels,
         "timing": timing,
         "clock": clock,

@@ -342,3 +342,19 @@ def test_python_mask_size_matches_c_abi(monkeypatch):
     assert fa._mask_cap() == 1 << 30
     monkeypatch.setenv("FA_V100_DROPOUT_MASK_MAX_BYTES", "0")
     assert fa._mask_cap() == 0
+
+
+def test_bench_step_roofline():
+    """bench.py's whole-step roofline: config 2 (B=8 H=12 S=4096) is MFMA-bound at 1188.5
+    flop/B on the operation's minimum bytes (12 fp16 tensors + 2 fp32 rows); the S=512 bucket
+    of config 3 (B=64) is HBM-bound there at 8 TB/s x 148.6 flop/B = 1188.5 TFLOP/s."""
+    import bench
+    f2 = 7 * 8 * 12 * 4096 * 4096 * 64
+    r = bench.step_roofline(8, 12, 4096, f2, 700.0)
+    assert r["minimum"]["algorithmic_bytes"] == 12 * 8 * 12 * 4096 * 128 + 2 * 8 * 12 * 4096 * 4
+    assert r["minimum"]["bound"] == "mfma" and r["minimum"]["attainable"] == round(bench.PEAK_TFLOPS, 1)
+    assert abs(r["minimum"]["intensity_flop_per_byte"] - 1188.5) < 0.1
+    r = bench.step_roofline(64, 12, 512, 7 * 64 * 12 * 512 * 512 * 64, 360.0)
+    assert r["minimum"]["bound"] == "hbm" and abs(r["minimum"]["attainable"] - 1188.5) < 0.1
+    assert r["split_design"]["algorithmic_bytes"] == 16 * 64 * 12 * 512 * 128 + 8 * 64 * 12 * 512 * 4
+    assert abs(r["minimum"]["frac"] - 360.0 / r["minimum"]["attainable"]) < 1e-4
