@@ -1140,12 +1140,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv_pipe_kernel(const BwdArgs a) {
         j = L / BH;
         bh = L - j * BH;
     }
-    // Single blocks: j = 0, the heaviest under the causal mask, first.  Pairs:
-    // every other workgroup runs its short block first, so that the
-    // workgroups sharing a CU, which start together and carry equal work, do
-    // not also reach their block change (the next block's first loads, the
-    // previous one's stores) at the same time.
-    const bool swap = pair && ((L >> 3) & 1);
+    // Single blocks: j = 0, the heaviest under the causal mask, first.  Pairs
+    // of short blocks (nkb <= 8: S <= 1024): every other workgroup runs its
+    // short block first, so that the workgroups sharing a CU, which start
+    // together and carry equal work, do not also reach their block change
+    // (the next block's first loads, the previous one's stores) at the same
+    // time.  Longer sequences keep one order: a head's workgroups then stream
+    // the same query tiles at about the same time, which keeps them in L2.
+    const bool swap = pair && nkb <= 8 && ((L >> 3) & 1);
     const int ja = swap ? nkb - 1 - j : j, jb = swap ? j : nkb - 1 - j;
     dkv_block<CAUSAL, DROPOUT, FOLD, DMASK>(a, ja, bh);
     if (pair && jb != ja) {
