@@ -346,7 +346,7 @@ def test_config2_full_shape(fa):
     _check_sampled_heads(fa, "config2", q, k, v, do, [(0, 0), (7, 11), (3, 5)])
 
 
-@pytest.mark.parametrize("S", [512, 1024, 2048])
+@pytest.mark.parametrize("S", [512, 1024, 2048, 4096])
 def test_config3_buckets(fa, S):
     say(f"case config 3 S={S}")
     q, k, v, do = wl.config_inputs(f"3-{S}", device=DEV)
