@@ -39,8 +39,8 @@ __device__ __forceinline__ int64_t row_term_word(int S, int bh, int q, int which
 }
 // Writes both terms of query q (lse2 = LSE * log2(e)).
 __device__ __forceinline__ void store_row_terms(const BwdArgs &a, int bh, int q, float lse2, float delta) {
-    a.trip[row_term_word(a.S, bh, q, 0)] = __builtin_bit_cast(uint32_t, -lse2 / a.scale2);
-    a.trip[row_term_word(a.S, bh, q, 1)] = __builtin_bit_cast(uint32_t, -delta);
+    a.rowterm[row_term_word(a.S, bh, q, 0)] = -lse2 / a.scale2;
+    a.rowterm[row_term_word(a.S, bh, q, 1)] = -delta;
 }
 
 // ---------------------------------------------------------------------------
@@ -800,7 +800,7 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     // recomputed with 64-bit multiplies at every transfer.
     uint64_t gq = (uint64_t)(uintptr_t)(Qp + (int64_t)q_start * a.qss);
     uint64_t gdo = (uint64_t)(uintptr_t)(dOp + (int64_t)q_start * a.doss);
-    uint64_t gld = FOLD ? (uint64_t)(uintptr_t)(a.trip + row_term_word(S, bh, q_start, 0))
+    uint64_t gld = FOLD ? (uint64_t)(uintptr_t)(a.rowterm + row_term_word(S, bh, q_start, 0))
                         : (uint64_t)(uintptr_t)(a.delta + (int64_t)bh * S + q_start);
     const uint32_t ldoff_t = FOLD ? 4u * (uint32_t)lane : ldoff;
     const uint64_t dq_step = (uint64_t)KP_QT * a.qss * 2, ddo_step = (uint64_t)KP_QT * a.doss * 2;

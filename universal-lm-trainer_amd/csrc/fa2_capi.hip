@@ -308,7 +308,7 @@ static int bwd_run(const fa2_bwd_params *p, int32_t mode, void *workspace, void 
     a.dv = static_cast<_Float16 *>(p->dv);
     a.delta = static_cast<float *>(workspace);
     a.lse2 = a.delta + (int64_t)p->B * p->H * p->S;
-    a.trip = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S));
+    a.rowterm = reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S));
     a.dqacc = fused ? reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S) +
                                                 terms_bytes(p->B, p->H, p->S))
                     : nullptr;

@@ -284,8 +284,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // take the true row max, rescale O and l, and form P again.  l and LSE
     // use whatever msc is current, so the result is the exact online softmax;
     // the reference max only bounds the magnitudes (P <= 2^15).
+    // The lane's partial row sum is kept as four sums, one per (kb, hh) group
+    // of eight elements, added pairwise at the end: four short dependency
+    // chains of v_dot2 instead of one of sixteen.  (The pipelined step sums
+    // the same elements in the same order, so both loops give the same bits.)
     auto p_form = [&](const f16x(&s)[2], float sub, h8(&pb)[2][2]) FA2_INLINE {
-        float rs = 0.f;
+        float part[4];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -294,9 +298,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hh + e], scale2, -sub));
                 pb[kb][hh] = __builtin_convertvector(x, h8);
-                rs = sum_h8(pb[kb][hh], rs);
+                part[2 * kb + hh] = sum_h8(pb[kb][hh], 0.f);
             }
-        return rs;
+        return (part[0] + part[1]) + (part[2] + part[3]);
     };
     // After P of tile k0 (K tile in `stage`) was formed with partial sum rs:
     // the cold path (scores recomputed from the K tile, so no score register
@@ -389,8 +393,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         // chunk i >= 4: scores for d-step i - 4, key blocks 0 and 1; each for
         // every query block, with the operand fragments shared.
         h8 n0 = vread(sv, 0, 0, 0), n1 = vread(sv, 1, 0, 0);
+        float part[QB][4];
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) rs[qb] = 0.f;
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part[qb][j] = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const h8 f0 = n0, f1 = n1;
@@ -423,11 +430,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) p_cur[qb][kb2][hh2][e0 + e] = ph[e];
                 const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-                rs[qb] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 0, 1), one, rs[qb], false);
-                rs[qb] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 2, 3), one, rs[qb], false);
+                float &pj = part[qb][i >> 1];   // group (kb2, hh2)
+                pj = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 0, 1), one, pj, false);
+                pj = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 2, 3), one, pj, false);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) rs[qb] = (part[qb][0] + part[qb][1]) + (part[qb][2] + part[qb][3]);
     };
 
     // Software pipeline over key tiles:

@@ -43,7 +43,7 @@ struct BwdArgs {
     // 32): the block's 32 values of -LSE*log2(e)/scale2, then its 32 values of
     // -delta, fp32 -- the per-row terms the dK/dV pass starts its S and dP
     // accumulators from.
-    uint32_t *trip;
+    float *rowterm;
     float *dqacc;        // [B*H, S, 64] fp32 dQ accumulator of the fused backward (or null)
     int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss;
     int64_t osb, osh, oss, dosb, dosh, doss;
