@@ -325,9 +325,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     f16x sA, dpA, sB, dpB;
     h8 dsA[2], dsB[2];
     {
-        // Step t reads only tile t: tiles t+1 .. t+3 may be in flight.  Tile 3
-        // goes out now; each tile end waits for the next tile only and
-        // refills the stage just read with tile t+4.
+        // Tiles are computed in pairs with one barrier after each pair: while
+        // tiles t-1, t are read, t+1, t+2 are in flight; the pair's end waits
+        // for those two (every issued transfer) and refills the two stages
+        // just read with tiles t+3, t+4.  Tile 3 goes out now.
         constexpr int TPT = DMASK ? 6 : 4;   // transfers per tile and wave
         if (QP_NST - 1 < ntiles) issue(QP_NST - 1);
         auto wait_pending = [&](int n) FA2_INLINE {
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
             else if (n == 2) vm_wait<2 * TPT>();
             else vm_wait<3 * TPT>();
         };
-        wait_pending(min(QP_NST - 1, ntiles - 1));
+        wait_pending(min(QP_NST - 2, ntiles - 2));   // tiles 0 and 1 landed
         lds_barrier();
         for (int t = 0; t < ntiles; ++t) {
             const int st = stage_of(t);
@@ -376,18 +377,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
                         }
                 }
             }
-            if (t < ntiles - 1) {
-                wait_pending(min(QP_NST - 2, ntiles - 2 - t));   // tile t+1 landed
+            if ((t & 1) && t < ntiles - 1) {   // the end of a pair, not the last tile
+                vm_wait<0>();                  // tiles t+1, t+2 (the next pair) landed
                 lds_barrier();
-                if (t + QP_NST < ntiles) issue(t + QP_NST);
+                if (t + 3 < ntiles) issue(t + 3);
+                if (t + 4 < ntiles) issue(t + 4);
             }
         }
     }
 
-    // dQ rows leave through LDS (store_rows_f16).  The last tile has no
-    // barrier after it, so other waves may still read the stage of tile
-    // ntiles-1; stages ntiles % 4 and (ntiles + 1) % 4 are idle (their last
-    // reads precede an earlier barrier, and every transfer has landed): waves
+    // dQ rows leave through LDS (store_rows_f16).  The last pair (or single
+    // last tile) has no barrier after it, so other waves may still read the
+    // stages of tiles ntiles-2 and ntiles-1; stages ntiles % 4 and
+    // (ntiles + 1) % 4 are idle (their last reads precede an earlier barrier,
+    // no later transfer refilled them, and every transfer has landed): waves
     // 0, 1 use the first, waves 2, 3 the second, 4 KB per 32-query block.
     static_assert(QP_NST == 4 && DQ_QB == 2 && sizeof(sKV[0]) == 16384, "dQ staging layout");
     const float sc = a.scale;

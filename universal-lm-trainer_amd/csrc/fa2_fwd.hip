@@ -448,10 +448,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // the stage of tile t-1 for tile t+NST-1.
     static_assert(NST == 4 || NST == 5, "three resident tiles plus one or two in flight");
     if constexpr (NOPIPE) {
-        // Step t reads only tile t, so tiles t+1 .. t+3 may be in flight
-        // meanwhile: tile 3 goes out now, and each tile end waits for the
-        // next tile only (2*TPW transfers per tile and wave) and refills the
-        // stage just read with tile t+4.
+        // Tiles are computed in pairs with one barrier after each pair: while
+        // tiles t-1, t are read, t+1, t+2 are in flight; the pair's end waits
+        // for those two (every issued transfer) and refills the two stages
+        // just read with tiles t+3, t+4.  Tile 3 goes out now.
         if (NST - 1 < ntiles) issue(NST - 1);
         auto wait_pending = [&](int n) FA2_INLINE {   // at most n tiles' transfers in flight
             if (n <= 0) vm_wait<0>();
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
             else if (n == 2) vm_wait<4 * TPW>();
             else vm_wait<6 * TPW>();
         };
-        wait_pending(min(NST - 1, ntiles - 1));
+        wait_pending(min(NST - 2, ntiles - 2));   // tiles 0 and 1 landed
         lds_barrier();
         f16x s[QB][2];
         h8 p[QB][2][2];
@@ -503,9 +503,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
                 }
                 pv(stage, p);
             }
-            wait_pending(min(NST - 2, ntiles - 2 - t));   // tile t+1 landed
-            lds_barrier();                                   // every wave is done with tile t
-            if (t + NST < ntiles) issue(t + NST);
+            if (!(t & 1) && t + 1 < ntiles) continue;   // the pair's first tile
+            vm_wait<0>();                                // tiles t+1, t+2 (the next pair) landed
+            lds_barrier();                               // every wave is done with tiles t-1, t
+            if (t + 3 < ntiles) issue(t + 3);
+            if (t + 4 < ntiles) issue(t + 4);
+            static_assert(!(NOPIPE && DMASK), "the paired loop stores no keep words");
             if (DMASK && t <= tlast) {
                 // Stored after the tile's transfers: the count-based waits
                 // never count a store (one issued after the awaited loads only
