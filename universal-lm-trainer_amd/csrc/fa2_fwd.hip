@@ -81,6 +81,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     constexpr bool NOPIPE = QBT == 2;
     static_assert(QBT == 1 || QBT == 2, "one or two query blocks per wave");
     static_assert(!DMASK || (DROPOUT && !SPLIT && NST == 4), "keep-bit words: the unsplit forward");
+    static_assert(!(DMASK && QBT == 2), "keep-bit words: the one-block (pipelined) loop");
     static_assert(!NOPIPE || NST == 4, "the unpipelined loop's waits assume four stages");
     // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
     __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
@@ -463,7 +464,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         lds_barrier();
         f16x s[QB][2];
         h8 p[QB][2][2];
-        uint32_t wq[QB] = {};   // DMASK: the keep words of the tile (one per query block)
         for (int t = 0; t < ntiles; ++t) {
             const int k0 = kbase + t * KT;
             const int stage = stage_of(t);
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
                         rs = p_form(s[qb], (mnew == -INFINITY) ? 0.f : mnew, p[qb]);
                     }
                     l[qb] += rs;
-                    if (DROPOUT) wq[qb] = drop_apply(qb, k0, p[qb]);
+                    if (DROPOUT) (void)drop_apply(qb, k0, p[qb]);
                 }
                 pv(stage, p);
             }
@@ -508,17 +508,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
             lds_barrier();                               // every wave is done with tiles t-1, t
             if (t + 3 < ntiles) issue(t + 3);
             if (t + 4 < ntiles) issue(t + 4);
-            static_assert(!(NOPIPE && DMASK), "the paired loop stores no keep words");
-            if (DMASK && t <= tlast) {
-                // Stored after the tile's transfers: the count-based waits
-                // never count a store (one issued after the awaited loads only
-                // makes a wait longer).
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    const int q = qw0 + 32 * qb + c;
-                    if (q < S) a.drop_mask[dmask_word(CAUSAL, bh, S, kbase / KT + t, g2, q)] = wq[qb];
-                }
-            }
         }
     } else {
     // Tiles 0 and 1 have landed once at most the transfers of tiles
