@@ -183,8 +183,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
             vo[i] = (uint32_t)(row * (int)a.vss + 8 * ch) * 2u;
         }
     };
-    // Tiles are issued in order, once each: scalar running addresses (global
-    // tile bases, LDS stage) advance by a constant per tile.
+    // Tiles are issued in order, once each: issue_next() sends the next tile
+    // (the callers' index tests only decide whether there is one).  Scalar
+    // running addresses (global tile bases, LDS stage) advance by a constant
+    // per tile.
     uint64_t gk = (uint64_t)(uintptr_t)Kp, gv = (uint64_t)(uintptr_t)Vp;
     const uint64_t k_step = (uint64_t)DQ_KT * a.kss * 2, v_step = (uint64_t)DQ_KT * a.vss * 2;
     int kn = 0;          // first key of the next tile to issue
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     // DMASK: the wave's 64 words per half g2 of each tile (rows past S are
     // within the mask's padded rows), 4 bytes per lane.
     const uint32_t lds_mq = lds_addr(&sMQ[0][wave][0][0]);
-    auto issue = [&](int) FA2_INLINE {
+    auto issue_next = [&]() FA2_INLINE {
         uint32_t ko[2], vo[2];
         tile_offsets(kn, ko, vo);
 #pragma unroll
@@ -215,7 +217,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     };
 #pragma unroll
     for (int t = 0; t < QP_NST - 1; ++t)
-        if (t < ntiles) issue(t);
+        if (t < ntiles) issue_next();
 
     // Resident Q^T / dO^T operands, delta and log2-scaled LSE of the wave's
     // queries (rows past S: row S - 1 and LSE = +inf, so P = dS = 0).
@@ -330,7 +332,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         // for those two (every issued transfer) and refills the two stages
         // just read with tiles t+3, t+4.  Tile 3 goes out now.
         constexpr int TPT = DMASK ? 6 : 4;   // transfers per tile and wave
-        if (QP_NST - 1 < ntiles) issue(QP_NST - 1);
+        if (QP_NST - 1 < ntiles) issue_next();
         auto wait_pending = [&](int n) FA2_INLINE {
             if (n <= 0) vm_wait<0>();
             else if (n == 1) vm_wait<TPT>();
@@ -380,8 +382,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
             if ((t & 1) && t < ntiles - 1) {   // the end of a pair, not the last tile
                 vm_wait<0>();                  // tiles t+1, t+2 (the next pair) landed
                 lds_barrier();
-                if (t + 3 < ntiles) issue(t + 3);
-                if (t + 4 < ntiles) issue(t + 4);
+                if (t + 3 < ntiles) issue_next();
+                if (t + 4 < ntiles) issue_next();
             }
         }
     }
@@ -798,9 +800,11 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     uint32_t qoff0, dooff0;
     tile_offsets(0, qoff0, dooff0);
     const uint32_t ldoff = ((lane < 32) ? (uint32_t)BH * (uint32_t)S * 4u : 0u) + 4u * (uint32_t)(lane & 31);
-    // Tiles are issued in order, once each: scalar running addresses (global
-    // tile bases, LDS stage) advance by a constant per tile instead of being
-    // recomputed with 64-bit multiplies at every transfer.
+    // Tiles are issued in order, once each: issue_next() sends the next tile
+    // (the callers' index tests only decide whether there is one).  Scalar
+    // running addresses (global tile bases, LDS stage) advance by a constant
+    // per tile instead of being recomputed with 64-bit multiplies at every
+    // transfer.
     uint64_t gq = (uint64_t)(uintptr_t)(Qp + (int64_t)q_start * a.qss);
     uint64_t gdo = (uint64_t)(uintptr_t)(dOp + (int64_t)q_start * a.doss);
     uint64_t gld = FOLD ? (uint64_t)(uintptr_t)(a.rowterm + row_term_word(S, bh, q_start, 0))
@@ -816,7 +820,7 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     // block have runs of one length; lanes 32..63 repeat lanes 0..31).
     const uint32_t dmoff = 4u * (uint32_t)(((lane & 31) >> 3) * dmask_run(CAUSAL, S, 2 * kblk) + 4 * (lane & 7));
     const uint32_t lds_dm = lds_addr(&sDM[0][0]);
-    auto issue = [&](int) FA2_INLINE {
+    auto issue_next = [&]() FA2_INLINE {
         uint32_t qo = qoff0, doo = dooff0;
         if (qn + KP_QT > S) tile_offsets(qn, qo, doo);
         lds_dma16_at(gq, qo, lds_qd + stn * (uint32_t)sizeof(sQD[0]));
@@ -833,7 +837,7 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
     };
 #pragma unroll
     for (int t = 0; t < KP_NST - 1; ++t)
-        if (t < ntiles) issue(t);
+        if (t < ntiles) issue_next();
     // Transfers per tile and wave: 2, plus 1 for wave 0 (and, DMASK, for
     // wave 1).  Wait until at most n tiles' transfers are pending.
     const bool three = wave == 0 || (DMASK && wave == 1);
@@ -847,7 +851,7 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
         // tile t+2 landed (tiles up to t+NST-2 issued); stage of tile t-1 free
         wait_tiles(min(KP_NST - 4, ntiles - 1 - (t + 2)));
         lds_barrier();
-        if (t + KP_NST - 1 < ntiles) issue(t + KP_NST - 1);
+        if (t + KP_NST - 1 < ntiles) issue_next();
     };
 
     f16x dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};   // dK^T, dV^T (d blocks)

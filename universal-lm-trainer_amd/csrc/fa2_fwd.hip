@@ -164,16 +164,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)NST); };
     uint32_t koffg[2], voffg[2];
     tile_offsets(0, koffg, voffg);
-    // Tiles are issued in order, once each: scalar running addresses (global
-    // tile bases, LDS stage) advance by a constant per tile instead of being
-    // recomputed with 64-bit multiplies at every transfer.
+    // Tiles are issued in order, once each: issue_next() sends the next tile
+    // (the callers' index tests only decide whether there is one).  Scalar
+    // running addresses (global tile bases, LDS stage) advance by a constant
+    // per tile instead of being recomputed with 64-bit multiplies at every
+    // transfer.
     uint64_t gk = (uint64_t)(uintptr_t)(Kp + (int64_t)kbase * a.kss);
     uint64_t gv = (uint64_t)(uintptr_t)(Vp + (int64_t)kbase * a.vss);
     const uint64_t k_step = (uint64_t)KT * a.kss * 2, v_step = (uint64_t)KT * a.vss * 2;
     int kn = kbase;      // first key of the next tile to issue
     uint32_t stn = 0;    // its stage
     const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 1024u * (uint32_t)(TPW * wave);
-    auto issue = [&](int) FA2_INLINE {
+    auto issue_next = [&]() FA2_INLINE {
         uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
         if (kn + KT > Sk) tile_offsets(kn, ko, vo);
 #pragma unroll
@@ -189,7 +191,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     };
 #pragma unroll
     for (int t = 0; t < NST - 1; ++t)
-        if (t < ntiles) issue(t);
+        if (t < ntiles) issue_next();
 
     f16x o[QB][2];                      // O^T, d blocks 0..31 and 32..63
     float msc[QB], l[QB];               // reference max (log2 units), per-lane partial row sum
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         // tiles t-1, t are read, t+1, t+2 are in flight; the pair's end waits
         // for those two (every issued transfer) and refills the two stages
         // just read with tiles t+3, t+4.  Tile 3 goes out now.
-        if (NST - 1 < ntiles) issue(NST - 1);
+        if (NST - 1 < ntiles) issue_next();
         auto wait_pending = [&](int n) FA2_INLINE {   // at most n tiles' transfers in flight
             if (n <= 0) vm_wait<0>();
             else if (n == 1) vm_wait<2 * TPW>();
@@ -506,8 +508,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
             if (!(t & 1) && t + 1 < ntiles) continue;   // the pair's first tile
             vm_wait<0>();                                // tiles t+1, t+2 (the next pair) landed
             lds_barrier();                               // every wave is done with tiles t-1, t
-            if (t + 3 < ntiles) issue(t + 3);
-            if (t + 4 < ntiles) issue(t + 4);
+            if (t + 3 < ntiles) issue_next();
+            if (t + 4 < ntiles) issue_next();
         }
     } else {
     // Tiles 0 and 1 have landed once at most the transfers of tiles
@@ -529,7 +531,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         if (NST == 5 && t + 3 < ntiles) vm_wait<4>();
         else if (t + 2 < ntiles) vm_wait<0>();
         lds_barrier();
-        if (t + NST - 1 < ntiles) issue(t + NST - 1);
+        if (t + NST - 1 < ntiles) issue_next();
         if (DMASK && t <= tlast) {
             const int q = qw0 + c;   // QB == 1
             if (q < S) a.drop_mask[dmask_word(CAUSAL, bh, S, kbase / KT + t, g2, q)] = wpend;
