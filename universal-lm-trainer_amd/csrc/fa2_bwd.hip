@@ -704,6 +704,9 @@ constexpr int KP_KWG = KP_NW * 32;    // keys per workgroup
 #endif
 constexpr int KP_NST = FA2_KV_NST;    // LDS stages: tiles t-1, t, t+1 resident, t+2 .. in flight (4..6)
 static_assert(KP_NST >= 4 && KP_NST <= 6, "dK/dV stages");
+// FOLD: the chunk (0..3) of a steady step in which the next tile's row terms
+// are read from LDS into its S and dP accumulators (two chunks ahead of their
+// first MFMA, so the reads are done by then).
 #ifndef FA2_KV_CINIT_CHUNK
 #define FA2_KV_CINIT_CHUNK 2
 #endif
