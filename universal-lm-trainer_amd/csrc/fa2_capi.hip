@@ -1,6 +1,8 @@
 // fa2_capi.hip -- the C ABI (include/fa2_mi355x.h): argument validation,
-// kernel-argument packing and launches.  Allocates nothing, keeps no state
-// besides a thread-local error message, never synchronises.
+// kernel-argument packing and launches.  Allocates nothing and never
+// synchronises; its only state is a thread-local error message, a per-device
+// cache of the compute-unit count, and the per-device scratch array of the
+// allocation-free backward.
 #include <float.h>
 #include <math.h>
 #include <stdarg.h>
