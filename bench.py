@@ -49,9 +49,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
     ap.add_argument("--no-dropout", action="store_true", help="skip the dropout p=0.1 timings")
-    ap.add_argument("--bwd-mode", type=int, default=7,
-                    help="fa_bwd mode of the timed step: 7 = split dQ pass (default), "
-                         "15 = fused backward with fp32 dQ atomics")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the secondary block that measures every other benchmark configuration "
+                         "(3 at S=512..4096, 4, trainer buckets S=4050 and S=1050, 5)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (3 launches) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
@@ -366,7 +366,7 @@ def decoder_step(args, torch, fa):
         def backward(ctx, do):
             q, k, v, o, lse = ctx.saved_tensors
             do = do if do.stride(3) == 1 else do.contiguous()
-            dq, dk, dv = timed(lambda: ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, 0.125, 0, args.bwd_mode))
+            dq, dk, dv = timed(lambda: ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, 0.125, 0, 7))
             return dq, dk, dv
 
     for layer in model.layers:
@@ -417,7 +417,7 @@ def decoder_step(args, torch, fa):
         "config": {"workload": f"config 5: {L}-layer decoder training step (d_model 768, 12 heads, SwiGLU 2048, "
                                f"vocab 32000, tied head) B={B} S={S}, fp16 autocast + GradScaler + fused AdamW; "
                                f"value = attention fwd+bwd rate inside the step",
-                   "B": B, "S": S, "layers": L, "bwd_mode": args.bwd_mode},
+                   "B": B, "S": S, "layers": L},
         "step": {"tokens_per_s": round(B * S / (ms_per_step / 1e3), 1),
                  "ms_median_events": round(ms_per_step, 3),
                  "ms_wall_mean": round(elapsed / args.steps * 1e3, 3),
@@ -484,6 +484,170 @@ def kv_forward(args, torch, fa):
     }
 
 
+def attention_case(args, torch, ext, B, H, S, q, k, v, do, steps, warmup, parity=True, extras=False):
+    """One configuration of the causal fwd+bwd step through the drop-in ops
+    (fa_fwd / fa_bwd, mode 7) on HBM-resident inputs:
+      * parity first: sampled heads (first and last) against SDPA MATH fp32
+        (O max-abs <= 2e-3, gradients <= 1e-2 relative); a failure ends the run;
+      * per-kernel launch durations: HIP events around each C-ABI launch (fwd,
+        dQ pass = mode 2, dK/dV pass = mode 4) on the launch stream, average and
+        median over max(steps, 5) launches after two untimed ones;
+      * the step: `warmup` untimed steps, then `steps` steps each bracketed by
+        HIP events on the stream; value = algorithmic flops / median step;
+      * the clock over 10 further steps (clock probe).
+    extras: also the cold-L2 step (median of 10, each after a 512 MB write)."""
+    import fa2_capi
+    import fa2_workloads as wl
+    dev = "cuda"
+    scale = 0.125
+    worst = None
+    if parity:
+        ok, worst = parity_gate(ext, q, k, v, do, [(0, 0), (B - 1, H - 1)])
+        print(f"parity B={B} H={H} S={S}: {worst} {'ok' if ok else 'FAILED'}", file=sys.stderr, flush=True)
+        if not ok:
+            raise SystemExit("parity gate failed: no performance report")
+    fwd_flops, bwd_flops = wl.causal_flops(B, H, S)
+    step_flops = fwd_flops + bwd_flops
+
+    def step():
+        o, lse = ext.fa_fwd(q, k, v, 0.0, True, scale, 0)
+        ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, scale, 0, 7)
+
+    stream = torch.cuda.current_stream()
+    # The parity check leaves the GPU idle while the host compares results, and
+    # the first ~100 ms of work after such a pause run several percent slow:
+    # untimed steps for 150 ms first, so that every timed figure sees the
+    # sustained state.
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.15:
+        step()
+        torch.cuda.synchronize()
+
+    lib = fa2_capi.load()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=dev)
+    dq, dk, dv = (torch.empty(B, H, S, 64, dtype=torch.float16, device=dev) for _ in range(3))
+    ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4 + 64, device=dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    pf = fa2_capi.fwd_params(q, k, v, o, lse, scale)
+    pb = fa2_capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, scale)
+    n = max(steps, 5)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
+    for i in range(n + 2):
+        e = ev[i - 2] if i >= 2 else None
+        if e: e[0].record(stream)
+        assert lib.fa2_fwd_f16(ctypes.byref(pf), sp) == 0, lib.fa2_last_error()
+        if e: e[1].record(stream)
+        assert lib.fa2_bwd_f16(ctypes.byref(pb), 2, ws.data_ptr(), ws.numel() * 4, sp) == 0, lib.fa2_last_error()
+        if e: e[2].record(stream)
+        assert lib.fa2_bwd_f16(ctypes.byref(pb), 4, ws.data_ptr(), ws.numel() * 4, sp) == 0, lib.fa2_last_error()
+        if e: e[3].record(stream)
+    torch.cuda.synchronize()
+    names = ("fwd", "bwd_dq", "bwd_dkv")
+    avg = {nm: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev) for j, nm in enumerate(names)}
+    med = {nm: statistics.median(e[j].elapsed_time(e[j + 1]) for e in ev) for j, nm in enumerate(names)}
+    del o, lse, dq, dk, dv, ws
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    sev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    sev[0].record(stream)
+    for i in range(steps):
+        step()
+        sev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    step_ms = [sev[i].elapsed_time(sev[i + 1]) for i in range(steps)]
+    ms_per_step = statistics.median(step_ms)
+    clock = clock_over_steps(torch, step, ms_per_step=ms_per_step)
+    value = step_flops / (ms_per_step / 1e3) / 1e12
+
+    unit = B * H * S * S * 64
+    executed = {"fwd": 2 * unit, "bwd_dq": 3 * unit, "bwd_dkv": 4 * unit}
+    kernels = {nm: {"avg_ms": round(avg[nm], 4), "median_ms": round(med[nm], 4),
+                    "executed_gflop": round(executed[nm] / 1e9, 2),
+                    "tflops": round(executed[nm] / (avg[nm] / 1e3) / 1e12, 1)} for nm in names}
+    timing = {"fwd_ms": round(avg["fwd"], 4), "bwd_ms": round(avg["bwd_dq"] + avg["bwd_dkv"], 4),
+              "fwd_bwd_ms": round(sum(avg.values()), 4),
+              "kernel_sum_median_ms": round(sum(med.values()), 4),
+              "step_ms": {"median": round(ms_per_step, 4), "min": round(min(step_ms), 4),
+                          "max": round(max(step_ms), 4), "mean": round(statistics.mean(step_ms), 4),
+                          "wall_mean": round(elapsed / steps * 1e3, 4),
+                          "sample": f"HIP events around each of the {steps} timed steps on the stream; "
+                                    f"wall_mean = host perf_counter over them / K"}}
+    if extras:
+        # Cold L2: each step preceded by a 512 MB buffer write (larger than the
+        # L2s and the MALL share a step touches), timed alone; median of 10.
+        flush = torch.empty(512 * 2**20 // 4, device=dev)
+        cold = []
+        for i in range(10):
+            flush.fill_(float(i))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            step()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            cold.append(e0.elapsed_time(e1))
+        del flush
+        cold_ms = statistics.median(cold)
+        timing["cold_l2"] = {"ms_per_step": round(cold_ms, 4),
+                             "tflops": round(step_flops / (cold_ms / 1e3) / 1e12, 1),
+                             "flush_mb": 512, "sample": "median of 10 steps, each after a 512 MB device write"}
+    return {"B": B, "H": H, "S": S, "ms_per_step": round(ms_per_step, 4), "tflops": round(value, 2),
+            "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+            "algorithmic_gflop_per_step": round(step_flops / 1e9, 2),
+            "step_roofline": step_roofline(B, H, S, step_flops, value), "kernels": kernels, "timing": timing,
+            "clock": clock, "parity": worst}
+
+
+# The secondary configurations of the default run: the benchmark's other
+# configurations plus two bucket lengths the reference's token-budget sampler
+# produces that are no multiple of 64 (bucket boundaries are multiples of
+# BUCKET_STEP = 50: reference @ None: train.py:1750-1858, 2587-2593), at
+# B*S ~ 32k tokens like configuration 3.
+BUCKETS = {"bucket-4050": dict(B=8, H=12, S=4050), "bucket-1050": dict(B=31, H=12, S=1050)}
+
+
+def configs_block(args, torch, fa, ext):
+    """Every other configuration, each with its own parity gate, median step,
+    per-kernel times and step roofline: 3 (S = 512, 1024, 2048, 4096), 4, the
+    two trainer buckets, and 5 (the 10-layer decoder step with the attention
+    time inside it, after its own parity gate).  20 timed steps each (5 for
+    configuration 5) after 5 warm-up steps."""
+    import fa2_workloads as wl
+    steps = min(args.steps, 20)
+    out = {}
+    for key in ("3-512", "3-1024", "3-2048", "3-4096", 4, "bucket-4050", "bucket-1050"):
+        if key in BUCKETS:
+            shape = BUCKETS[key]
+            B, H, S = shape["B"], shape["H"], shape["S"]
+            inputs = wl.make_inputs(B, H, S, seed=0, device="cuda")
+            desc = f"trainer bucket B={B} H={H} S={S} (S % 64 = {S % 64}), N(0,1)"
+        else:
+            cfg = wl.CONFIGS[key]
+            B, H, S = cfg["B"], cfg["H"], cfg["S"]
+            inputs = wl.config_inputs(key, device="cuda")
+            desc = f"config {key}: B={B} H={H} S={S}" + (", 1% of Q rows x8" if cfg["outlier_frac"] else "")
+        torch.cuda.synchronize()
+        case = attention_case(args, torch, ext, B, H, S, *inputs, steps=steps, warmup=5,
+                              parity=not args.no_parity)
+        case["workload"] = desc
+        out[str(key)] = case
+        del inputs
+        torch.cuda.empty_cache()
+        print(f"config {key}: {case['ms_per_step']} ms, {case['tflops']} TFLOP/s", file=sys.stderr, flush=True)
+    sub = argparse.Namespace(**vars(args))
+    sub.steps, sub.warmup = 5, 3
+    r5 = decoder_step(sub, torch, fa)
+    out["5"] = {"workload": r5["config"]["workload"], "attention_tflops": r5["value"],
+                "attention_pct_of_peak": r5["pct_of_peak"], "ms_per_step": r5["ms_per_step"],
+                "step": r5["step"], "clock": r5["clock"], "parity": r5["parity"], "steps": sub.steps}
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -519,131 +683,30 @@ def main():
     key = cfg_key(args.config)
     cfg = wl.CONFIGS[key]
     B, H, S = cfg["B"], cfg["H"], cfg["S"]
-    dev = "cuda"
-    q, k, v, do = wl.config_inputs(key, device=dev)
+    q, k, v, do = wl.config_inputs(key, device="cuda")
     torch.cuda.synchronize()
-
-    parity = None
-    if not args.no_parity:
-        ok, parity = parity_gate(ext, q, k, v, do, [(0, 0), (B - 1, H - 1)])
-        print(f"parity {parity} {'ok' if ok else 'FAILED'}", file=sys.stderr, flush=True)
-        if not ok:
-            raise SystemExit("parity gate failed: no performance report")
-
-    fwd_flops, bwd_flops = wl.causal_flops(B, H, S)
-    step_flops = fwd_flops + bwd_flops
-    scale = 0.125
-
-    def step():
-        o, lse = ext.fa_fwd(q, k, v, 0.0, True, scale, 0)
-        ext.fa_bwd(q, k, v, o, lse, do, 0.0, True, scale, 0, args.bwd_mode)
-
-    stream = torch.cuda.current_stream()
-
-    # The parity check leaves the GPU idle while the host compares results, and
-    # the first ~100 ms of work after such a pause run several percent slow:
-    # untimed steps for 150 ms first, so that every timed figure below sees the
-    # sustained state.
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < 0.15:
-        step()
-        torch.cuda.synchronize()
-
-    # Per-kernel launch durations: HIP events around each C-ABI launch on the
-    # current stream (the stream the kernels run on), over max(K, 5) steps after
-    # two untimed ones.
-    lib = fa2_capi.load()
-    o = torch.empty_like(q)
-    lse = torch.empty(B, H, S, device=dev)
-    dq, dk, dv = (torch.empty(B, H, S, 64, dtype=torch.float16, device=dev) for _ in range(3))
-    ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4, device=dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    pf = fa2_capi.fwd_params(q, k, v, o, lse, scale)
-    pb = fa2_capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, scale)
-    n = max(args.steps, 5)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
-    for i in range(n + 2):
-        e = ev[i - 2] if i >= 2 else None
-        if e: e[0].record(stream)
-        assert lib.fa2_fwd_f16(ctypes.byref(pf), sp) == 0, lib.fa2_last_error()
-        if e: e[1].record(stream)
-        assert lib.fa2_bwd_f16(ctypes.byref(pb), 2, ws.data_ptr(), ws.numel() * 4, sp) == 0
-        if e: e[2].record(stream)
-        assert lib.fa2_bwd_f16(ctypes.byref(pb), 4, ws.data_ptr(), ws.numel() * 4, sp) == 0
-        if e: e[3].record(stream)
-    torch.cuda.synchronize()
-    avg = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev)
-           for j, name in enumerate(("fwd", "bwd_dq", "bwd_dkv"))}
-    med = {name: statistics.median(e[j].elapsed_time(e[j + 1]) for e in ev)
-           for j, name in enumerate(("fwd", "bwd_dq", "bwd_dkv"))}
-    del o, lse, dq, dk, dv, ws
-
-    # The headline: W warm-up steps, then K steps through the drop-in ops, each
-    # bracketed by HIP events on the stream; value = flops / median step.  The
-    # host wall clock over the K steps (which adds launch and allocator time
-    # whenever the host falls behind the GPU) is kept as a secondary figure.
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    sev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    t0 = time.perf_counter()
-    sev[0].record(stream)
-    for i in range(args.steps):
-        step()
-        sev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    step_ms = [sev[i].elapsed_time(sev[i + 1]) for i in range(args.steps)]
-    clock = clock_over_steps(torch, step, ms_per_step=statistics.median(step_ms))
-    ms_per_step = statistics.median(step_ms)
-    value = step_flops / (ms_per_step / 1e3) / 1e12
-    wall_ms = elapsed / args.steps * 1e3
-
-    unit = B * H * S * S * 64
-    executed = {"fwd": 2 * unit, "bwd_dq": 3 * unit, "bwd_dkv": 4 * unit}
+    case = attention_case(args, torch, ext, B, H, S, q, k, v, do, steps=args.steps, warmup=args.warmup,
+                          parity=not args.no_parity, extras=True)
+    step_flops = sum(wl.causal_flops(B, H, S))
+    kernels, avg = case["kernels"], {n: case["kernels"][n]["avg_ms"] for n in case["kernels"]}
     dom = max(avg, key=avg.get)
-    achieved = executed[dom] / (avg[dom] / 1e3) / 1e12
-    kernels = {kname: {"avg_ms": round(avg[kname], 4), "median_ms": round(med[kname], 4),
-                       "executed_gflop": round(executed[kname] / 1e9, 2),
-                       "tflops": round(executed[kname] / (avg[kname] / 1e3) / 1e12, 1)} for kname in avg}
-
-    # Cold L2: each step preceded by a 512 MB buffer write (larger than the
-    # L2s and the MALL share a step touches), timed alone; median of 10.
-    flush = torch.empty(512 * 2**20 // 4, device=dev)
-    cold = []
-    for i in range(10):
-        flush.fill_(float(i))
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        step()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        cold.append(e0.elapsed_time(e1))
-    del flush
-    cold_ms = statistics.median(cold)
-    timing = {"fwd_ms": round(avg["fwd"], 4), "bwd_ms": round(avg["bwd_dq"] + avg["bwd_dkv"], 4),
-              "fwd_bwd_ms": round(sum(avg.values()), 4),
-              "kernel_sum_median_ms": round(sum(med.values()), 4),
-              "step_ms": {"median": round(ms_per_step, 4), "min": round(min(step_ms), 4),
-                          "max": round(max(step_ms), 4), "mean": round(statistics.mean(step_ms), 4),
-                          "wall_mean": round(wall_ms, 4),
-                          "sample": f"HIP events around each of the {args.steps} timed steps on the stream; "
-                                    f"wall_mean = host perf_counter over them / K"},
-              "cold_l2": {"ms_per_step": round(cold_ms, 4), "tflops": round(step_flops / (cold_ms / 1e3) / 1e12, 1),
-                          "flush_mb": 512, "sample": "median of 10 steps, each after a 512 MB device write"}}
+    achieved = kernels[dom]["tflops"]
     if not args.no_dropout:
-        timing["dropout"] = dropout_steps(torch, ext, q, k, v, do, scale, stream, step_flops)
-    timing["rope"] = rope_timing(torch, ext, B, H, S, stream)
+        case["timing"]["dropout"] = dropout_steps(torch, ext, q, k, v, do, 0.125, torch.cuda.current_stream(),
+                                                  step_flops)
+    case["timing"]["rope"] = rope_timing(torch, ext, B, H, S, torch.cuda.current_stream())
+    del q, k, v, do
+    torch.cuda.empty_cache()
 
     result = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": case["tflops"],
         "unit": "TFLOP/s",
-        "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "pct_of_peak": case["pct_of_peak"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": case["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -651,16 +714,17 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"causal FA-2 fwd+bwd, config {args.config}: B={B} H={H} S={S} D=64 fp16"
                                + (" RoPE inputs" if cfg["rope"] else ""),
-                   "B": B, "H": H, "S": S, "D": 64, "algorithmic_gflop_per_step": round(step_flops / 1e9, 2),
-                   "bwd_mode": args.bwd_mode},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": round(PEAK_TFLOPS, 1),
+                   "B": B, "H": H, "S": S, "D": 64, "algorithmic_gflop_per_step": round(step_flops / 1e9, 2)},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": round(PEAK_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(dom)},
-        "step_roofline": step_roofline(B, H, S, step_flops, value),
+        "step_roofline": case["step_roofline"],
         "kernels": kernels,
-        "timing": timing,
-        "clock": clock,
-        "parity": parity,
+        "timing": case["timing"],
+        "clock": case["clock"],
+        "parity": case["parity"],
     }
+    if not args.no_configs and args.config == "2":
+        result["configs"] = configs_block(args, torch, fa, ext)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

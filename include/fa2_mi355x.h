@@ -133,20 +133,16 @@ int fa2_fwd_kv_split_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_of
  * Replaces fav100::fa_bwd and its three kernels (delta, dQ, dK/dV)
  *   (reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:42-506).
  * `mode` keeps the reference's bit mask (bwd.cu:476-502), 1 = delta,
- * 2 = dQ, 4 = dK/dV, 7 = all, plus bit 8:
+ * 2 = dQ, 4 = dK/dV, 7 = all (0..7; anything else is FA2_ERR_BAD_ARGUMENT):
  *   - 7: split pass like the reference -- a dQ kernel that also writes delta,
  *     then the dK/dV kernel (no atomics, run-to-run identical);
  *   - 2: the dQ kernel (writes delta); 1: delta only; 4: dK/dV reading the
  *     delta and scaled LSE an earlier call (mode 1 or 2) left in the
- *     workspace;
- *   - 14 or 15 (bit 8 with dQ and dK/dV): fused backward -- delta and a
- *     cleared fp32 dQ accumulator, one dK/dV kernel that also adds dS K into
- *     the accumulator with fp32 atomics, then dQ = scale * accumulator.
- *     Slower on MI355X (the atomics are L2-throughput bound); kept selectable.
+ *     workspace.
  * The workspace (fa2_bwd_workspace_bytes) holds delta[b,h,i] = sum_d O*dO and
- * LSE[b,h,i] * log2(e) in fp32, the per-row terms -LSE*log2(e)/scale2 and
+ * LSE[b,h,i] * log2(e) in fp32 and the per-row terms -LSE*log2(e)/scale2 and
  * -delta that start the dK/dV step's accumulators (all written by the dQ or
- * delta step, read by the dK/dV step) and the fp32 dQ accumulator.  B*H*S must be below 2^30. */
+ * delta step, read by the dK/dV step).  B*H*S must be below 2^30. */
 typedef struct fa2_bwd_params {
     const void *q, *k, *v, *o, *dout;   /* fp16 [B,H,S,64]                     */
     const float *lse;                   /* fp32 [B,H,S] from the forward       */
@@ -160,24 +156,22 @@ typedef struct fa2_bwd_params {
     uint32_t seed;
     int32_t causal;
     const uint32_t *dropout_mask;       /* optional: fa2_fwd_f16's keep bits (see
-                                           fa2_dropout_mask_bytes); read by the
-                                           split backward (modes 2, 4, 7), while
-                                           the fused backward hashes again, with
-                                           the same result; NULL = hash           */
+                                           fa2_dropout_mask_bytes), read by the dQ
+                                           and dK/dV kernels instead of the hash,
+                                           with the same result; NULL = hash      */
     size_t dropout_mask_bytes;          /* bytes at dropout_mask, checked like the
                                            forward's                              */
 } fa2_bwd_params;
 
 /* Workspace bytes fa2_bwd_f16 needs for (B, H, S): fp32 delta and scaled LSE
- * (8*B*H*S bytes, rounded up to 256), the row terms -LSE*log2(e)/scale2 and
- * -delta in fp32 (8*B*H*ceil32(S) bytes, rounded up to 256),
- * then the fp32 dQ accumulator (256*B*H*S bytes). */
+ * (8*B*H*S bytes, rounded up to 256), then the row terms -LSE*log2(e)/scale2
+ * and -delta in fp32 (8*B*H*ceil32(S) bytes, rounded up to 256). */
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S);
 
 int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,
                 size_t workspace_bytes, void *stream);
 
-/* Allocation-free backward: fa2_bwd_f16 (modes 0..7, same kernels, same
+/* Allocation-free backward: fa2_bwd_f16 (same modes, same kernels, same
  * results bit for bit) with no workspace argument.  Its workspace is scratch
  * memory inside the library: a device array of FA2_BWD_SCRATCH_MAX_BYTES that
  * every GPU the library runs on holds from the first use until the process
@@ -185,17 +179,18 @@ int fa2_bwd_f16(const fa2_bwd_params *p, int32_t mode, void *workspace,
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc); the caller still provides inputs and outputs.
  *   - Size limit: fa2_bwd_noalloc_scratch_bytes(B, H, S) (delta, scaled LSE and
- *     the row terms: about 16*B*H*S bytes) must not exceed
- *     FA2_BWD_SCRATCH_MAX_BYTES, else FA2_ERR_WORKSPACE; the fused backward
- *     (mode bit 8, which needs a 256*B*H*S-byte accumulator) is rejected with
- *     FA2_ERR_BAD_ARGUMENT.
+ *     the row terms: about 16*B*H*S bytes, the same as fa2_bwd_workspace_bytes)
+ *     must not exceed FA2_BWD_SCRATCH_MAX_BYTES, else FA2_ERR_WORKSPACE.
+ *   - Set-up: the device address of the array is looked up once per device, on
+ *     the first call with that device current (a symbol lookup that may load the
+ *     library's code object; it allocates nothing).  A caller that captures the
+ *     call into a HIP graph makes one call on that device before capturing.
  *   - Sharing: all calls on one GPU share that GPU's array, which keeps the last
  *     call's contents.  Calls that overlap in time on one GPU (several streams
  *     or host threads) race on it and must be serialised by the caller.  Mode 4
  *     reads the delta an earlier mode 1 or 2 call left there, so that pair must
  *     run back to back on one stream with no other call in between.
- * No counterpart in the reference: its fa_bwd allocates its delta buffer and
- * outputs per call (reference @ None: csrc/flash_attn_v100/flash_attn_v100_bwd.cu:461-464). */
+ * No counterpart in the reference; for callers that cannot allocate. */
 #define FA2_BWD_SCRATCH_MAX_BYTES (32u << 20)
 size_t fa2_bwd_noalloc_scratch_bytes(int32_t B, int32_t H, int32_t S);
 int fa2_bwd_f16_noalloc(const fa2_bwd_params *p, int32_t mode, void *stream);

@@ -34,7 +34,7 @@ def say(*a):
 
 
 def run_kernel(fa, q, k, v, do, causal=True, scale=0.125, p=0.0, seed=0, mode=7):
-    """mode 7 = split dQ pass (default), 15 = fused backward with fp32 dQ atomics."""
+    """fa_bwd `mode`: the reference's bit mask (1 delta, 2 dQ, 4 dK/dV; 7 = all)."""
     ext = fa.extension()
     o, lse = ext.fa_fwd(q, k, v, p, causal, scale, seed)
     dq, dk, dv = ext.fa_bwd(q, k, v, o, lse, do, p, causal, scale, seed, mode)
@@ -86,12 +86,11 @@ def rand_inputs(B, H, S, seed, scale=1.0):
 
 @pytest.mark.parametrize("S", [1, 2, 17, 63, 64, 65, 127, 129, 200, 256, 257, 300, 513])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("mode", [7, 15])
-def test_small_shapes_vs_oracle(fa, S, causal, mode):
-    say(f"case small S={S} causal={causal} mode={mode}")
+def test_small_shapes_vs_oracle(fa, S, causal):
+    say(f"case small S={S} causal={causal}")
     q, k, v, do = rand_inputs(1, 2, S, seed=S + 1000 * causal)
-    got = run_kernel(fa, q, k, v, do, causal=causal, mode=mode)
-    check_against(f"S={S} causal={causal} mode={mode}", got, oracle_ref(q, k, v, do, causal, 0.125))
+    got = run_kernel(fa, q, k, v, do, causal=causal)
+    check_against(f"S={S} causal={causal}", got, oracle_ref(q, k, v, do, causal, 0.125))
 
 
 def test_golden_fixtures(fa):
@@ -136,11 +135,10 @@ def test_row_term_extremes(fa, scale, amp, S):
 
 
 @pytest.mark.parametrize("p,seed", [(0.1, 1), (0.5, 0xC0FFEE), (0.9, 42)])
-@pytest.mark.parametrize("mode", [7, 15])
-def test_dropout_vs_oracle(fa, p, seed, mode):
-    say(f"case dropout p={p} seed={seed} mode={mode}")
+def test_dropout_vs_oracle(fa, p, seed):
+    say(f"case dropout p={p} seed={seed}")
     q, k, v, do = rand_inputs(2, 2, 160, seed=seed % 1000)
-    got = run_kernel(fa, q, k, v, do, p=p, seed=seed, mode=mode)
+    got = run_kernel(fa, q, k, v, do, p=p, seed=seed)
     # Dropout scales O by 1/(1-p); the fp16 output's own rounding scales with
     # it, so the O bar does too (grads keep the relative bar).
     check_against(f"dropout p={p}", got, oracle_ref(q, k, v, do, True, 0.125, p=p, seed=seed),
@@ -202,7 +200,7 @@ def test_capi_direct_matches_binding(fa):
     assert lib.fa2_fwd_f16(ctypes.byref(p), stream) == 0, lib.fa2_last_error()
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
     ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4, device=DEV)
-    assert ws.numel() * 4 >= B * H * S * 4 + B * H * S * 256
+    assert ws.numel() * 4 >= B * H * S * 8 + B * H * ((S + 31) // 32 * 32) * 8   # delta, LSE*log2e, row terms
     pb = capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, 0.125)
     assert lib.fa2_bwd_f16(ctypes.byref(pb), 7, ws.data_ptr(), ws.numel() * 4, stream) == 0
     torch.cuda.synchronize()
@@ -290,37 +288,15 @@ def test_capi_split_modes(fa):
 
 
 def test_deterministic(fa):
-    """The forward and the split backward are run-to-run identical; the fused
-    backward is too for dK/dV, while its dQ sums fp32 atomics in arrival order
-    and matches the split pass within rounding."""
+    """The forward and the backward are run-to-run identical, and fa_bwd, like
+    the reference's, reads only bits 1, 2 and 4 of `mode` (mode 15 = mode 7)."""
     say("case determinism")
     q, k, v, do = rand_inputs(2, 4, 777, seed=3)
     a = run_kernel(fa, q, k, v, do, mode=7)
     b = run_kernel(fa, q, k, v, do, mode=7)
-    for x, y in zip(a, b):
-        assert torch.equal(x, y)
-    f1 = run_kernel(fa, q, k, v, do, mode=15)
-    f2 = run_kernel(fa, q, k, v, do, mode=15)
-    for i in (0, 1, 3, 4):
-        assert torch.equal(f1[i], f2[i])
-    # the two kernel variants may contract/round differently: compare closely, not bitwise
-    for i in range(5):
-        ref = a[i].float()
-        for got in (f1[i], f2[i]):
-            err = ((got.float() - ref).norm() / ref.norm()).item()
-            assert err < 2e-3, (i, err)
-
-
-@pytest.mark.parametrize("causal", [True, False])
-def test_fused_matches_split_medium(fa, causal):
-    say(f"case fused vs split B=2 H=3 S=1100 causal={causal}")
-    q, k, v, do = rand_inputs(2, 3, 1100, seed=17)
-    fused = run_kernel(fa, q, k, v, do, causal=causal, mode=15)
-    split = run_kernel(fa, q, k, v, do, causal=causal, mode=7)
-    for i, n in enumerate(("o", "lse", "dq", "dk", "dv")):
-        e = ((fused[i].float() - split[i].float()).norm() / split[i].float().norm()).item()
-        say(f"fused vs split {n} rel {e:.2e}")
-        assert e < 2e-3, n
+    c = run_kernel(fa, q, k, v, do, mode=15)
+    for x, y, z in zip(a, b, c):
+        assert torch.equal(x, y) and torch.equal(x, z)
 
 
 def _check_sampled_heads(fa, name, q, k, v, do, heads):

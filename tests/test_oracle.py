@@ -6,7 +6,9 @@ independent integer evaluation of the dropout hash.  A mistake planted in a
 copy of the oracle (dropped delta term, wrong scale placement) is shown to
 fail the invariant checks.
 """
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -317,10 +319,34 @@ def test_dropout_statistics():
     assert (keep[0, 0] != keep[0, 0].T).mean() > 0.1           # row/col not symmetric
 
 
-def test_seed_formula():
-    assert orc.next_seed(0, 1) == 1
-    assert orc.next_seed(1, 1) == (2654435761 + 1) & 0xFFFFFFFF
-    assert orc.next_seed(2 ** 40 + 3, 7) == ((2 ** 40 + 3) * 2654435761 + 7) % 2 ** 32
+def _seed_golden():
+    with open(os.path.join(os.path.dirname(__file__), "golden", "seed_golden.json")) as f:
+        return json.load(f)["cases"]
+
+
+def test_seed_formula_against_reference_vectors():
+    """orc.next_seed against the seeds the reference's own _next_seed returned
+    (tests/golden/make_seed_golden.py imported flash_attn_v100_cuda.py:28-33):
+    14 initial seeds, including 64-bit ones, five counter values each."""
+    cases = _seed_golden()
+    assert len(cases) >= 10 and any(c["initial_seed"] >= 2 ** 32 for c in cases)
+    for c in cases:
+        assert [orc.next_seed(c["initial_seed"], i) for i in range(1, len(c["seeds"]) + 1)] == c["seeds"]
+
+
+def test_seed_vectors_catch_planted_mistakes():
+    """The vectors fail a seed formula with a mistyped multiplier, the counter
+    starting at 0, the counter xor-ed instead of added, or a 31-bit mask."""
+    cases = _seed_golden()
+
+    def agrees(f):
+        return all([f(c["initial_seed"], i) for i in range(1, 6)] == c["seeds"] for c in cases)
+
+    assert agrees(orc.next_seed)
+    assert not agrees(lambda s, i: (s * 2654435769 + i) & 0xFFFFFFFF)
+    assert not agrees(lambda s, i: (s * 2654435761 + i - 1) & 0xFFFFFFFF)
+    assert not agrees(lambda s, i: ((s * 2654435761) ^ i) & 0xFFFFFFFF)
+    assert not agrees(lambda s, i: (s * 2654435761 + i) & 0x7FFFFFFF)
 
 
 def _rotate_half(x):
@@ -436,3 +462,24 @@ def test_kv_fwd_decode_closed_form():
     s = np.einsum("bhid,bhjd->bhij", q, k) * 0.2
     assert orc.max_abs(o, np.einsum("bhij,bhjd->bhid", softmax(s, axis=-1), v)) < 1e-12
     assert orc.max_abs(lse, logsumexp(s, axis=-1)) < 1e-12
+
+
+def test_reference_hash_recipe_takes_exactly_the_hash_lines():
+    """oracle/build_ref.py compiles the reference's hash_u32 and dropout_keep
+    (fa_common.cuh:21-38) and nothing else of the header; when the reference
+    tree is present the extraction is checked here, and when the checker
+    library is present it must export both harness entry points."""
+    import ctypes
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("fa2_build_ref", os.path.join(orc.__file__.rsplit("/", 1)[0], "build_ref.py"))
+    br = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(br)
+    if br.available():
+        with open(br.HEADER) as f:
+            first, block = br.extract_hash_lines(f.read())
+        text = "\n".join(block)
+        assert (first, first + len(block) - 1) == (21, 38)
+        assert "hash_u32" in text and "dropout_keep" in text and "#include" not in text
+    if os.path.exists(br.LIB):
+        lib = ctypes.CDLL(br.LIB)
+        assert hasattr(lib, "fa2ref_dropout_keep") and hasattr(lib, "fa2ref_hash_u32")

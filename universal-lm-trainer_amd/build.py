@@ -6,9 +6,6 @@ Produces, next to this file under ``lib/``:
   * ``_fa2_torch<EXT_SUFFIX>`` -- the thin PyTorch-ROCm extension exposing the
     reference's ``fa_fwd``/``fa_bwd``/``rope_fwd``/``rope_bwd`` ops on top of
     that C ABI (g++, linked with an ``$ORIGIN`` rpath);
-  * ``probe_dq_atomics`` -- a stand-alone measurement of the fp32-atomic dQ
-    accumulation traffic a fused backward would issue (the evidence behind
-    the split dQ pass), run under rocprofv3;
   * ``libfa2_clock_probe.so`` -- bench.py's in-process clock reading (a
     one-wave s_memtime / s_memrealtime probe; not part of the C ABI).
 
@@ -108,19 +105,6 @@ def build_extension(verbose=False):
     return ext_path()
 
 
-def probe_path():
-    return os.path.join(LIB, "probe_dq_atomics")
-
-
-def build_probe(verbose=False):
-    tmp = probe_path() + ".tmp"
-    out = _run([HIPCC, *[f for f in HIP_FLAGS if f != "-fPIC"], os.path.join(CSRC, "probe_dq_atomics.hip"), "-o", tmp])
-    if verbose and out.strip():
-        print(out)
-    os.replace(tmp, probe_path())
-    return probe_path()
-
-
 def clock_probe_path():
     return os.path.join(LIB, "libfa2_clock_probe.so")
 
@@ -137,9 +121,8 @@ def build_clock_probe(verbose=False):
 def build(verbose=False):
     build_library(verbose)
     build_extension(verbose)
-    build_probe(verbose)
     build_clock_probe(verbose)
-    return lib_path(), ext_path(), probe_path(), clock_probe_path()
+    return lib_path(), ext_path(), clock_probe_path()
 
 
 if __name__ == "__main__":

@@ -22,7 +22,7 @@
 //     V^T in registers), streams query tiles (Q, dO row-major, lse, delta via
 //     LDS; Q^T and dO^T operands through transposing reads) and accumulates
 //     dK^T and dV^T in registers; P and dS feed the dV/dK MFMAs straight from
-//     the S/dP accumulators.  (bwd_dkv_kernel<FUSE> is the atomic-dQ variant.)
+//     the S/dP accumulators.
 #include "fa2_device.h"
 #include "fa2_kernels.h"
 
@@ -71,32 +71,6 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const BwdArgs a) {
             store_row_terms(a, bh, row, l2, sum);
         }
     }
-    if (a.dqacc && row < S) {  // fused backward: clear this row of the fp32 dQ accumulator
-        f4 *z = reinterpret_cast<f4 *>(a.dqacc + ((int64_t)bh * S + row) * HD + 8 * part);
-        const f4 zero = {0.f, 0.f, 0.f, 0.f};
-        z[0] = zero;
-        z[1] = zero;
-    }
-}
-
-// dQ = fp16(scale * accumulator), 8 lanes per row (fused backward epilogue).
-__global__ __launch_bounds__(256) void bwd_dq_convert_kernel(const BwdArgs a) {
-    const int S = a.S;
-    const int nrb = (S + 31) / 32;
-    const int bh = blockIdx.x / nrb;
-    const int row = (blockIdx.x - bh * nrb) * 32 + (threadIdx.x >> 3);
-    if (row >= S) return;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int part = threadIdx.x & 7;
-    const f4 *src = reinterpret_cast<const f4 *>(a.dqacc + ((int64_t)bh * S + row) * HD + 8 * part);
-    const f4 x0 = src[0], x1 = src[1];
-    f8 y;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        y[e] = x0[e] * a.scale;
-        y[4 + e] = x1[e] * a.scale;
-    }
-    *reinterpret_cast<h8 *>(a.dq + b * a.dqsb + h * a.dqsh + row * a.dqss + 8 * part) = __builtin_convertvector(y, h8);
 }
 
 // ---------------------------------------------------------------------------
@@ -402,295 +376,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     for (int qb = 0; qb < DQ_QB; ++qb)
         store_rows_f16(dq[qb][0], dq[qb][1], sc, stg + 4096 * qb, dQp + (int64_t)(qw0 + 32 * qb) * a.dqss, a.dqss,
                        S - (qw0 + 32 * qb), dq16);
-}
-
-// ---------------------------------------------------------------------------
-// dK / dV pass
-// ---------------------------------------------------------------------------
-constexpr int KV_NW = 4;
-constexpr int KV_KB = 1;                    // 32-key blocks per wave
-constexpr int KV_QT = 64;                   // queries per tile
-constexpr int KV_KWG = KV_NW * 32 * KV_KB;  // keys per workgroup
-
-template <bool CAUSAL, bool DROPOUT, bool FUSE>
-__global__ __launch_bounds__(256, 2) void bwd_dkv_kernel(const BwdArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 sQ[2][KV_QT * LDR];
-    __shared__ __attribute__((aligned(16))) _Float16 sdO[2][KV_QT * LDR];
-    __shared__ __attribute__((aligned(16))) float sL[2][KV_QT];
-    __shared__ __attribute__((aligned(16))) float sD[2][KV_QT];
-    // Fused dQ: K rows of this workgroup's keys (B operand of dQ = dS K) and the
-    // tile's dS^T [key][query] (A operand, read transposed).
-    __shared__ __attribute__((aligned(16))) _Float16 sKw[FUSE ? KV_KWG * LDR : 8];
-    __shared__ __attribute__((aligned(16))) _Float16 sdSt[FUSE ? KV_KWG * LDR : 8];
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g2 = lane >> 5;
-    const int S = a.S;
-    const int BH = a.B * a.H;
-    const int L = blockIdx.x;
-    const int kblk = L / BH;
-    const int bh = L - kblk * BH;
-    const int b = bh / a.H, h = bh - b * a.H;
-
-    const _Float16 *Qp = a.q + b * a.qsb + h * a.qsh;
-    const _Float16 *Kp = a.k + b * a.ksb + h * a.ksh;
-    const _Float16 *Vp = a.v + b * a.vsb + h * a.vsh;
-    const _Float16 *dOp = a.dout + b * a.dosb + h * a.dosh;
-    const float *Lp = a.lse + b * a.lsb + h * a.lsh;
-    const float *Dp = a.delta + (int64_t)bh * S;
-    _Float16 *dKp = a.dk + b * a.dksb + h * a.dksh;
-    _Float16 *dVp = a.dv + b * a.dvsb + h * a.dvsh;
-
-    const int k_wg0 = kblk * KV_KWG;
-    const int kw0 = k_wg0 + wave * 32 * KV_KB;
-    const float scale2 = a.scale2;
-
-    // Resident K^T / V^T B operands: lane holds key (kw0 + 32*kb + c).
-    h8 kf[KV_KB][4], vf[KV_KB][4];
-#pragma unroll
-    for (int kb = 0; kb < KV_KB; ++kb) {
-        const int key = kw0 + 32 * kb + c;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            h8 kv = zero_h8(), vv = zero_h8();
-            if (key < S) {
-                kv = *reinterpret_cast<const h8 *>(Kp + key * a.kss + 16 * st + 8 * g2);
-                vv = *reinterpret_cast<const h8 *>(Vp + key * a.vss + 16 * st + 8 * g2);
-            }
-            kf[kb][st] = a.negate ? neg_h8(kv) : kv;
-            vf[kb][st] = vv;
-        }
-    }
-
-    f16x dk[KV_KB][2], dv[KV_KB][2];
-#pragma unroll
-    for (int kb = 0; kb < KV_KB; ++kb) {
-        dk[kb][0] = zero16();
-        dk[kb][1] = zero16();
-        dv[kb][0] = zero16();
-        dv[kb][1] = zero16();
-    }
-
-    const int q_start = CAUSAL ? (k_wg0 / KV_QT) * KV_QT : 0;
-    const int ntiles = (k_wg0 < S) ? (S - q_start + KV_QT - 1) / KV_QT : 0;
-
-    const int lp = tid >> 3;
-    const int lc = (tid & 7) * 8;
-    h8 qr0, qr1, dr0, dr1;
-    float lr = 0.f, drr = 0.f;
-    auto gload = [&](int q0) {
-        const int r0 = q0 + 2 * lp, r1 = r0 + 1;
-        qr0 = zero_h8();
-        qr1 = zero_h8();
-        dr0 = zero_h8();
-        dr1 = zero_h8();
-        if (r0 < S) {
-            qr0 = *reinterpret_cast<const h8 *>(Qp + r0 * a.qss + lc);
-            dr0 = *reinterpret_cast<const h8 *>(dOp + r0 * a.doss + lc);
-        }
-        if (r1 < S) {
-            qr1 = *reinterpret_cast<const h8 *>(Qp + r1 * a.qss + lc);
-            dr1 = *reinterpret_cast<const h8 *>(dOp + r1 * a.doss + lc);
-        }
-        if (tid < KV_QT) {
-            const int q = q0 + tid;
-            lr = q < S ? Lp[q] * LOG2E : INFINITY;
-            drr = q < S ? Dp[q] : 0.f;
-        }
-    };
-    auto lstore = [&](int buf) {
-        *reinterpret_cast<h8 *>(&sQ[buf][(2 * lp) * LDR + lc]) = qr0;
-        *reinterpret_cast<h8 *>(&sQ[buf][(2 * lp + 1) * LDR + lc]) = qr1;
-        *reinterpret_cast<h8 *>(&sdO[buf][(2 * lp) * LDR + lc]) = dr0;
-        *reinterpret_cast<h8 *>(&sdO[buf][(2 * lp + 1) * LDR + lc]) = dr1;
-        if (tid < KV_QT) {
-            sL[buf][tid] = lr;
-            sD[buf][tid] = drr;
-        }
-    };
-
-    if (FUSE) {
-        // K rows [k_wg0, k_wg0 + KV_KWG) into LDS, zero past S (un-negated K: dQ = scale dS K).
-#pragma unroll
-        for (int it = 0; it < KV_KWG * 8 / 256; ++it) {
-            const int idx = tid + 256 * it;
-            const int r = idx >> 3, ch = (idx & 7) * 8;
-            h8 kv = zero_h8();
-            if (k_wg0 + r < S) kv = *reinterpret_cast<const h8 *>(Kp + (k_wg0 + r) * a.kss + ch);
-            *reinterpret_cast<h8 *>(&sKw[r * LDR + ch]) = kv;
-        }
-    }
-    // dS^T rows of this lane's key for query block qb (zeros where nothing is computed)
-    _Float16 *dst_row = sdSt + (FUSE ? (32 * wave + c) * LDR : 0);
-    auto write_ds_zero = [&](int qb) {
-        const h4 z = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<h4 *>(dst_row + 32 * qb + 8 * i + 4 * g2) = z;
-    };
-    const bool key_valid = kw0 + c < S;
-
-    if (ntiles > 0) {
-        gload(q_start);
-        lstore(0);
-    }
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        const int q0 = q_start + t * KV_QT;
-        if (t + 1 < ntiles) gload(q0 + KV_QT);
-
-        const bool active = (kw0 < S) && (!CAUSAL || q0 + KV_QT - 1 >= kw0);
-        if (FUSE && !active) {
-            write_ds_zero(0);
-            write_ds_zero(1);
-        }
-        if (active) {
-            const _Float16 *tQ = sQ[buf];
-            const _Float16 *tdO = sdO[buf];
-#pragma unroll
-            for (int qb = 0; qb < KV_QT / 32; ++qb) {
-                if (CAUSAL && q0 + 32 * qb + 31 < kw0) {  // whole block above the diagonal
-                    if (FUSE) write_ds_zero(qb);
-                    continue;
-                }
-                // S = Q K^T and dP = dO V^T : rows = queries, cols = this lane's key.
-                f16x s[KV_KB], dp[KV_KB];
-#pragma unroll
-                for (int kb = 0; kb < KV_KB; ++kb) {
-                    s[kb] = zero16();
-                    dp[kb] = zero16();
-                }
-#pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const h8 qa = *reinterpret_cast<const h8 *>(tQ + (32 * qb + c) * LDR + 16 * st + 8 * g2);
-                    const h8 da = *reinterpret_cast<const h8 *>(tdO + (32 * qb + c) * LDR + 16 * st + 8 * g2);
-#pragma unroll
-                    for (int kb = 0; kb < KV_KB; ++kb) {
-                        s[kb] = mfma32(qa, kf[kb][st], s[kb]);
-                        dp[kb] = mfma32(da, vf[kb][st], dp[kb]);
-                    }
-                }
-                f4 l4[4], d4[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    l4[i] = *reinterpret_cast<const f4 *>(&sL[buf][32 * qb + 8 * i + 4 * g2]);
-                    d4[i] = *reinterpret_cast<const f4 *>(&sD[buf][32 * qb + 8 * i + 4 * g2]);
-                }
-                const bool need_mask = CAUSAL && (q0 + 32 * qb < kw0 + 32 * KV_KB - 1);
-                h8 pb[KV_KB][2], dsb[KV_KB][2];
-                if (need_mask) {
-                    FA2_COLD_BRANCH();
-#pragma unroll
-                    for (int kb = 0; kb < KV_KB; ++kb) {
-                        const int key = kw0 + 32 * kb + c;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int q = q0 + 32 * qb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                            if (key > q) s[kb][r] = -INFINITY;
-                        }
-                    }
-                }
-#pragma unroll
-                for (int kb = 0; kb < KV_KB; ++kb) {
-                    const int key = kw0 + 32 * kb + c;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int q = q0 + 32 * qb + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale2, -l4[r >> 2][r & 3]));
-                        const float del = d4[r >> 2][r & 3];
-                        float pd = p, ds;
-                        if (DROPOUT) {
-                            const bool keep = dropout_keep(a.seed, q, key, (uint32_t)bh, a.drop_thr);
-                            pd = keep ? p * a.inv_keep : 0.f;
-                            ds = pd * dp[kb][r] - p * del;
-                        } else {
-                            ds = p * (dp[kb][r] - del);
-                        }
-                        s[kb][r] = pd;
-                        dp[kb][r] = ds;
-                    }
-                    pb[kb][0] = acc_to_h8(s[kb], 0);
-                    pb[kb][1] = acc_to_h8(s[kb], 1);
-                    dsb[kb][0] = acc_to_h8(dp[kb], 0);
-                    dsb[kb][1] = acc_to_h8(dp[kb], 1);
-                }
-                if (FUSE) {
-                    // dS^T[key][q]: registers 8hh..8hh+7 hold queries 16hh + 8*(e>>2) + 4*g2 + (e&3)
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        h8 v = dsb[0][hh];
-                        if (!key_valid) v = zero_h8();
-                        const h4 lo = {v[0], v[1], v[2], v[3]};
-                        const h4 hi = {v[4], v[5], v[6], v[7]};
-                        *reinterpret_cast<h4 *>(dst_row + 32 * qb + 16 * hh + 4 * g2) = lo;
-                        *reinterpret_cast<h4 *>(dst_row + 32 * qb + 16 * hh + 8 + 4 * g2) = hi;
-                    }
-                }
-                // dV^T += dO^T P and dK^T += Q^T dS, contracting 16 queries per step.
-#pragma unroll
-                for (int db = 0; db < 2; ++db)
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const h8 da = tr_read8<LDR>(tdO, 32 * qb + 16 * hh, 32 * db);
-                        const h8 qa = tr_read8<LDR>(tQ, 32 * qb + 16 * hh, 32 * db);
-#pragma unroll
-                        for (int kb = 0; kb < KV_KB; ++kb) {
-                            dv[kb][db] = mfma32(da, pb[kb][hh], dv[kb][db]);
-                            dk[kb][db] = mfma32(qa, dsb[kb][hh], dk[kb][db]);
-                        }
-                    }
-            }
-        }
-
-        if (FUSE) {
-            // dQ[q0 .. q0+63][0..63] += dS[64 x KV_KWG] K[KV_KWG x 64]: one 32x32 block per
-            // wave over all of this workgroup's keys, added to the fp32 accumulator.
-            __syncthreads();  // every wave's dS^T is in LDS
-            const int qb2 = wave >> 1, db = wave & 1;
-            f16x acc;
-#pragma unroll
-            for (int ks = 0; ks < KV_KWG / 16; ++ks) {
-                const h8 da = tr_read8<LDR>(sdSt, 16 * ks, 32 * qb2);
-                const h8 kb8 = tr_read8<LDR>(sKw, 16 * ks, 32 * db);
-                acc = ks == 0 ? mfma32_first(da, kb8) : mfma32(da, kb8, acc);
-            }
-            float *accrow = a.dqacc + ((int64_t)bh * S + q0 + 32 * qb2) * HD + 32 * db + c;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int r = 8 * i + 4 * g2 + j;
-                    if (q0 + 32 * qb2 + r < S)
-                        __hip_atomic_fetch_add(accrow + r * HD, acc[4 * i + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-        }
-        if (t + 1 < ntiles) lstore(buf ^ 1);
-        __syncthreads();
-    }
-
-    const float sc = a.scale;
-#pragma unroll
-    for (int kb = 0; kb < KV_KB; ++kb) {
-        const int key = kw0 + 32 * kb + c;
-        if (key < S) {
-            _Float16 *krow = dKp + key * a.dkss;
-            _Float16 *vrow = dVp + key * a.dvss;
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    f4 xk, xv;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        xk[j] = dk[kb][db][4 * i + j] * sc;
-                        xv[j] = dv[kb][db][4 * i + j];
-                    }
-                    *reinterpret_cast<h4 *>(krow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xk, h4);
-                    *reinterpret_cast<h4 *>(vrow + 32 * db + 8 * i + 4 * g2) = __builtin_convertvector(xv, h4);
-                }
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1199,23 +884,6 @@ hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_
     return hipGetLastError();
 }
 
-template <bool FUSE>
-static void launch_dkv_t(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
-    const int nkblk = (a.S + KV_KWG - 1) / KV_KWG;
-    const dim3 grid((unsigned)(nkblk * a.B * a.H)), block(256);
-    if (causal) {
-        if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_kernel<true, true, FUSE>), grid, block, 0, st, a);
-        else
-            hipLaunchKernelGGL((bwd_dkv_kernel<true, false, FUSE>), grid, block, 0, st, a);
-    } else {
-        if (dropout)
-            hipLaunchKernelGGL((bwd_dkv_kernel<false, true, FUSE>), grid, block, 0, st, a);
-        else
-            hipLaunchKernelGGL((bwd_dkv_kernel<false, false, FUSE>), grid, block, 0, st, a);
-    }
-}
-
 hipError_t launch_bwd_dkv(const BwdArgs &a_in, bool causal, bool dropout, hipStream_t st) {
     BwdArgs a = a_in;
     const int nkblk = (a.S + KP_KWG - 1) / KP_KWG;
@@ -1250,17 +918,6 @@ hipError_t launch_bwd_dkv(const BwdArgs &a_in, bool causal, bool dropout, hipStr
         else
             hipLaunchKernelGGL((bwd_dkv_pipe_kernel<false, false, false, false>), grid, block, 0, st, a);
     }
-    return hipGetLastError();
-}
-
-hipError_t launch_bwd_fused(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
-    launch_dkv_t<true>(a, causal, dropout, st);
-    return hipGetLastError();
-}
-
-hipError_t launch_bwd_dq_convert(const BwdArgs &a, hipStream_t st) {
-    const int nrb = (a.S + 31) / 32;
-    hipLaunchKernelGGL(bwd_dq_convert_kernel, dim3((unsigned)(nrb * a.B * a.H)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

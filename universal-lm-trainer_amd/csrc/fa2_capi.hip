@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "../../include/fa2_mi355x.h"
@@ -86,15 +87,17 @@ int check_mask(const void *mask, size_t bytes, int32_t B, int32_t H, int32_t S, 
 
 namespace fa2 {
 int device_cus() {
-    static int cached[64] = {};
+    // Relaxed atomics: racing first calls on several host threads each store
+    // the same value.
+    static std::atomic<int> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (!n) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;   // idempotent: racing first calls store the same value
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 }  // namespace fa2
 
@@ -240,9 +243,8 @@ int fa2_fwd_kv_split_f16(const fa2_fwd_params *p, int32_t s_k, int32_t causal_of
 }
 
 // Workspace: fp32 delta and log2-scaled LSE, [B*H*S] each (rounded up to 256
-// bytes); the per-row terms -LSE*log2(e)/scale2 and -delta in fp32, 8 bytes
-// per query with S rounded up to 32 (rounded up to 256 bytes); then the fp32
-// dQ accumulator [B*H*S*64] of the fused backward.
+// bytes), then the per-row terms -LSE*log2(e)/scale2 and -delta in fp32, 8
+// bytes per query with S rounded up to 32 (rounded up to 256 bytes).
 static size_t delta_bytes(int32_t B, int32_t H, int32_t S) {
     return ((size_t)B * H * S * 2 * sizeof(float) + 255) & ~(size_t)255;
 }
@@ -252,14 +254,14 @@ static size_t terms_bytes(int32_t B, int32_t H, int32_t S) {
 
 size_t fa2_bwd_workspace_bytes(int32_t B, int32_t H, int32_t S) {
     if (B <= 0 || H <= 0 || S <= 0) return 0;
-    return delta_bytes(B, H, S) + terms_bytes(B, H, S) + (size_t)B * H * S * FA2_HEAD_DIM * sizeof(float);
+    return delta_bytes(B, H, S) + terms_bytes(B, H, S);
 }
 
 // Checks of fa2_bwd_f16 that come before its workspace: status, or -1 when
 // the call has nothing to do (empty problem or mode 0) and returns FA2_OK.
 static int bwd_precheck(const fa2_bwd_params *p, int32_t mode) {
     if (!p) return fail(FA2_ERR_NULL_POINTER, "params is NULL");
-    if (mode < 0 || mode > 15) return fail(FA2_ERR_BAD_ARGUMENT, "mode %d outside 0..15", mode);
+    if (mode < 0 || mode > 7) return fail(FA2_ERR_BAD_ARGUMENT, "mode %d outside 0..7", mode);
     int rc = check_shape(p->B, p->H, p->S, p->D, 256);
     if (rc) return rc;
     if ((rc = check_scale_dropout(p->softmax_scale, p->dropout_p))) return rc;
@@ -270,12 +272,11 @@ static int bwd_precheck(const fa2_bwd_params *p, int32_t mode) {
     return FA2_OK;
 }
 
-// The backward on a workspace already checked to hold what `mode` uses:
-// delta, scaled LSE and row terms, plus the dQ accumulator when fused.
+// The backward on a workspace already checked to hold delta, the scaled LSE
+// and the row terms.
 static int bwd_run(const fa2_bwd_params *p, int32_t mode, void *workspace, void *stream) {
     int rc;
     const bool want_delta = mode & 1, want_dq = mode & 2, want_dkv = mode & 4;
-    const bool fused = want_dq && want_dkv && (mode & 8);
     if ((rc = check_tensor("o", p->o, p->o_stride, p->B, p->H, p->S, true))) return rc;
     if ((rc = check_tensor("dout", p->dout, p->do_stride, p->B, p->H, p->S, true))) return rc;
     if (want_dq || want_dkv) {
@@ -311,9 +312,6 @@ static int bwd_run(const fa2_bwd_params *p, int32_t mode, void *workspace, void 
     a.delta = static_cast<float *>(workspace);
     a.lse2 = a.delta + (int64_t)p->B * p->H * p->S;
     a.rowterm = reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S));
-    a.dqacc = fused ? reinterpret_cast<float *>(static_cast<char *>(workspace) + delta_bytes(p->B, p->H, p->S) +
-                                                terms_bytes(p->B, p->H, p->S))
-                    : nullptr;
     a.qsb = p->q_stride[0]; a.qsh = p->q_stride[1]; a.qss = p->q_stride[2];
     a.ksb = p->k_stride[0]; a.ksh = p->k_stride[1]; a.kss = p->k_stride[2];
     a.vsb = p->v_stride[0]; a.vsh = p->v_stride[1]; a.vss = p->v_stride[2];
@@ -335,16 +333,6 @@ static int bwd_run(const fa2_bwd_params *p, int32_t mode, void *workspace, void 
     const hipStream_t st = (hipStream_t)stream;
 
     hipError_t e = hipSuccess;
-    if (fused) {
-        // delta + cleared accumulator, then dK/dV with dQ accumulated by atomics, then dQ = scale * acc
-        e = fa2::launch_bwd_delta(a, st);
-        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "delta launch: %s", hipGetErrorString(e));
-        e = fa2::launch_bwd_fused(a, causal, dropout, st);
-        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "fused backward launch: %s", hipGetErrorString(e));
-        e = fa2::launch_bwd_dq_convert(a, st);
-        if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "dQ convert launch: %s", hipGetErrorString(e));
-        return FA2_OK;
-    }
     if (want_dq) {
         e = fa2::launch_bwd_dq(a, causal, dropout, st);  // also writes delta
         if (e != hipSuccess) return fail(FA2_ERR_LAUNCH, "dQ launch: %s", hipGetErrorString(e));
@@ -419,9 +407,6 @@ int fa2_bwd_f16_noalloc(const fa2_bwd_params *p, int32_t mode, void *stream) {
     g_err[0] = 0;
     int rc = bwd_precheck(p, mode);
     if (rc) return rc < 0 ? FA2_OK : rc;
-    if ((mode & 14) == 14)
-        return fail(FA2_ERR_BAD_ARGUMENT, "mode %d: the fused backward (bit 8) needs an fp32 dQ accumulator; "
-                    "fa2_bwd_f16_noalloc runs the split backward only", mode);
     const size_t need = fa2_bwd_noalloc_scratch_bytes(p->B, p->H, p->S);
     if (need > (size_t)FA2_BWD_SCRATCH_MAX_BYTES)
         return fail(FA2_ERR_WORKSPACE, "B=%d H=%d S=%d needs %zu bytes of scratch; fa2_bwd_f16_noalloc holds "

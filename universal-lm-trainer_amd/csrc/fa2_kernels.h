@@ -44,7 +44,6 @@ struct BwdArgs {
     // -delta, fp32 -- the per-row terms the dK/dV pass starts its S and dP
     // accumulators from.
     float *rowterm;
-    float *dqacc;        // [B*H, S, 64] fp32 dQ accumulator of the fused backward (or null)
     int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss;
     int64_t osb, osh, oss, dosb, dosh, doss;
     int64_t dqsb, dqsh, dqss, dksb, dksh, dkss, dvsb, dvsh, dvss;
@@ -89,8 +88,6 @@ hipError_t launch_fwd_decode(const FwdArgs &a, bool causal, hipStream_t st);
 hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);
 hipError_t launch_bwd_dkv(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);
-hipError_t launch_bwd_fused(const BwdArgs &a, bool causal, bool dropout, hipStream_t st);
-hipError_t launch_bwd_dq_convert(const BwdArgs &a, hipStream_t st);
 hipError_t launch_rope(const RopeArgs &a, bool backward, hipStream_t st);
 
 }  // namespace fa2

@@ -28,6 +28,9 @@ namespace fa2 {
 namespace {
 
 typedef float f8v __attribute__((ext_vector_type(8)));
+// cos / sin rows are only guaranteed 16-byte alignment (the host's vector-path
+// check), so their 8-float loads go through a type of that alignment.
+typedef float f8v_a16 __attribute__((ext_vector_type(8), aligned(16)));
 
 // One row of eight halves per lane: x = own halves, xp = partner halves,
 // cs / snv = cos and the sine the formula multiplies (own index forward,
@@ -64,10 +67,10 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(const RopeArgs a) {
     const int h = (int)(r - bs * H);
     const int b = (int)(bs / S), s = (int)(bs - (uint32_t)b * S);
     const float *csr = a.cs + (int64_t)s * a.cs0, *snr = a.sn + (int64_t)s * a.sn0;
-    const f8v cs = *reinterpret_cast<const f8v *>(csr + 8 * j);
+    const f8v cs = *reinterpret_cast<const f8v_a16 *>(csr + 8 * j);
     // forward: sin at the own index, partner sign -1 for d < 32;
     // backward: sin at the partner index, partner sign +1 for d < 32.
-    const f8v snv = *reinterpret_cast<const f8v *>(snr + 8 * (BACKWARD ? (j ^ 4) : j));
+    const f8v snv = *reinterpret_cast<const f8v_a16 *>(snr + 8 * (BACKWARD ? (j ^ 4) : j));
     const float sg = (j < 4) == BACKWARD ? 1.f : -1.f;
     const h8 xq = *reinterpret_cast<const h8 *>(a.q + b * a.qsb + h * a.qsh + s * a.qss + 8 * j);
     const h8 xk = *reinterpret_cast<const h8 *>(a.k + b * a.ksb + h * a.ksh + s * a.kss + 8 * j);

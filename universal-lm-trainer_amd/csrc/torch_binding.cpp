@@ -184,7 +184,9 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     TORCH_CHECK(lse.dtype() == torch::kFloat && lse.dim() == 3 && lse.size(0) == q.size(0) &&
                     lse.size(1) == q.size(1) && lse.size(2) == q.size(2),
                 "lse must be fp32 (B,H,S)");
-    TORCH_CHECK(mode >= 0 && mode <= 15, "mode must be a bit mask in 0..15");
+    // The reference tests bits 1, 2 and 4 of mode and ignores the rest
+    // (flash_attn_v100_bwd.cu:476-502).
+    TORCH_CHECK(mode >= 0, "mode must be a non-negative bit mask");
     check_dims(q, "fa_bwd");
     if (mask && dropout_p > 0.0) {
         TORCH_CHECK(mask->is_cuda() && mask->device() == q.device() && mask->dtype() == torch::kInt &&
@@ -246,7 +248,7 @@ std::vector<torch::Tensor> fa_bwd(torch::Tensor q, torch::Tensor k, torch::Tenso
     }
     // The workspace is fresh each call, so a dK/dV-only request also computes
     // delta (the reference would read an uninitialised buffer there).
-    int32_t m = (int32_t)mode;
+    int32_t m = (int32_t)(mode & 7);
     if ((m & 4) && !(m & 3)) m |= 1;
     check_status(fa2_bwd_f16(&p, m, ws.data_ptr(), (size_t)ws.numel() * 4, current_stream(q)), "fa_bwd");
     return {dq, dk, dv};
