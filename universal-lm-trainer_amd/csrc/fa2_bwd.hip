@@ -95,19 +95,34 @@ constexpr int QP_NST = 4;   // LDS stages: key tile t read, t+1 .. t+3 in flight
 // DMASK (dropout with a.drop_mask): the keep bits come from the words the
 // forward wrote (two per query and key tile, moved into LDS with the tile)
 // instead of the hash.
-template <bool CAUSAL, bool DROPOUT, bool DMASK>
-__global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
+//
+// NARROW: one 32-query block per wave (128 queries per workgroup), the same
+// in-order tile body, NSK = 2 or 3 LDS stages with one barrier per tile, and
+// at most 128 or 168 registers per lane, so that four or three workgroups
+// (waves per SIMD) share a CU and cover each other's latencies.
+#ifndef FA2_DQ_NARROW_WAVES
+#define FA2_DQ_NARROW_WAVES 3
+#endif
+constexpr int DQ_NARROW_WAVES = FA2_DQ_NARROW_WAVES;
+static_assert(DQ_NARROW_WAVES == 3 || DQ_NARROW_WAVES == 4, "three or four narrow waves per SIMD");
+
+template <bool CAUSAL, bool DROPOUT, bool DMASK, bool NARROW = false>
+__global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     static_assert(!DMASK || DROPOUT, "keep-bit words only with dropout");
-    __shared__ __attribute__((aligned(16))) h8 sKV[QP_NST][2][DQ_KT * 8];
-    // DMASK: per stage and wave, the words of its 64 queries for halves g2 = 0, 1.
-    __shared__ __attribute__((aligned(16))) uint32_t sMQ[DMASK ? QP_NST : 1][DQ_NW][2][64];
+    constexpr int QB = NARROW ? 1 : DQ_QB;            // 32-query blocks per wave
+    constexpr int QWG = DQ_NW * 32 * QB;              // queries per workgroup
+    constexpr int NSK = NARROW ? (DQ_NARROW_WAVES == 4 ? 2 : 3) : QP_NST;   // LDS stages
+    __shared__ __attribute__((aligned(16))) h8 sKV[NSK][2][DQ_KT * 8];
+    // DMASK: per stage and wave, the words of its 64 queries (32 when NARROW)
+    // for halves g2 = 0, 1.
+    __shared__ __attribute__((aligned(16))) uint32_t sMQ[DMASK ? NSK : 1][DQ_NW][2][64];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, c = lane & 31, g2 = lane >> 5;
     const int S = a.S;
     const int BH = a.B * a.H;
-    const int nqblk = (S + DQ_QWG - 1) / DQ_QWG;
+    const int nqblk = (S + QWG - 1) / QWG;
     const int L = blockIdx.x;
     const int qblk = nqblk - 1 - L / BH;   // heaviest (last) query blocks first
     const int bh = L - (L / BH) * BH;
@@ -122,21 +137,21 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     _Float16 *dQp = a.dq + b * a.dqsb + h * a.dqsh;
     float *Dp = a.delta + (int64_t)bh * S;
 
-    const int q_wg0 = qblk * DQ_QWG;
-    const int qw0 = q_wg0 + wave * 32 * DQ_QB;
+    const int q_wg0 = qblk * QWG;
+    const int qw0 = q_wg0 + wave * 32 * QB;
     const float scale2 = a.scale2;
 
     // The first key tiles go out before the wave's Q, dO and O rows are
     // loaded: the delta computation waits for those rows, and with the
     // transfers already in flight the two round trips overlap.
-    const int kend = CAUSAL ? min(S, q_wg0 + DQ_QWG) : S;
+    const int kend = CAUSAL ? min(S, q_wg0 + QWG) : S;
     const int ntiles = (kend + DQ_KT - 1) / DQ_KT;
     // Last key tile of this wave (-1: none).  The wave's first query is a
     // multiple of the tile size, so only that tile can need a mask.
-    const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32 * DQ_QB, S) - 1) / DQ_KT : ntiles - 1;
+    const int tlast = (qw0 >= S) ? -1 : CAUSAL ? (min(qw0 + 32 * QB, S) - 1) / DQ_KT : ntiles - 1;
 
     // Stage of tile t (t >= 0; unsigned, so a power-of-two count is a mask).
-    auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)QP_NST); };
+    auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)NSK); };
     // Tile loader (direct global->LDS transfers): wave w moves transfers
     // j = 2w, 2w+1 of the K and the V tile; lane L of transfer j lands at
     // chunk position 64j + L = 8*row + (L & 7), row = 8j + (L >> 3), and
@@ -166,8 +181,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     int kn = 0;          // first key of the next tile to issue
     uint32_t stn = 0;    // its stage
     const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 2048u * (uint32_t)wave;
-    // DMASK: the wave's 64 words per half g2 of each tile (rows past S are
-    // within the mask's padded rows), 4 bytes per lane.
+    // DMASK: the wave's 64 (NARROW: 32) words per half g2 of each tile (rows
+    // past S are within the mask's padded rows), 4 bytes per lane.
     const uint32_t lds_mq = lds_addr(&sMQ[0][wave][0][0]);
     auto issue_next = [&]() FA2_INLINE {
         uint32_t ko[2], vo[2];
@@ -182,23 +197,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
 #pragma unroll
             for (int half = 0; half < 2; ++half)
                 lds_dma4_at((uint64_t)(uintptr_t)(a.drop_mask + dmask_word(CAUSAL, bh, S, kn / DQ_KT, half, qw0)),
-                            4u * (uint32_t)lane, lds_mq + stn * (uint32_t)sizeof(sMQ[0]) + 256u * (uint32_t)half);
+                            4u * (uint32_t)(NARROW ? (lane & 31) : lane),   // NARROW: 32 words, lanes 32.. repeat
+                            lds_mq + stn * (uint32_t)sizeof(sMQ[0]) + 256u * (uint32_t)half);
         }
         gk += k_step;
         gv += v_step;
         kn += DQ_KT;
-        stn = (stn + 1 == QP_NST) ? 0 : stn + 1;
+        stn = (stn + 1 == NSK) ? 0 : stn + 1;
     };
 #pragma unroll
-    for (int t = 0; t < QP_NST - 1; ++t)
+    for (int t = 0; t < NSK - 1; ++t)
         if (t < ntiles) issue_next();
 
     // Resident Q^T / dO^T operands, delta and log2-scaled LSE of the wave's
     // queries (rows past S: row S - 1 and LSE = +inf, so P = dS = 0).
-    h8 qf[DQ_QB][4], dof[DQ_QB][4];
-    float lse2[DQ_QB], dl[DQ_QB];
+    h8 qf[QB][4], dof[QB][4];
+    float lse2[QB], dl[QB];
 #pragma unroll
-    for (int qb = 0; qb < DQ_QB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         const int q = qw0 + 32 * qb + c;
         const bool valid = q < S;
         const int qr = min(q, S - 1);
@@ -223,9 +239,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         }
     }
 
-    f16x dq[DQ_QB][2];
+    f16x dq[QB][2];
 #pragma unroll
-    for (int qb = 0; qb < DQ_QB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         dq[qb][0] = zero16();
         dq[qb][1] = zero16();
     }
@@ -300,20 +316,72 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
     // Query block qb's units keep S, dP and dS in role qb (A: 0, B: 1).
     f16x sA, dpA, sB, dpB;
     h8 dsA[2], dsB[2];
-    {
+    constexpr int TPT = DMASK ? 6 : 4;   // transfers per tile and wave
+    if constexpr (NARROW) {
+        // One query block: per 32 keys (kb) of tile t, S and dP, dS, then dQ.
+        // NSK stages: tile t is read while tiles t+1 .. t+NSK-1 are in
+        // flight; the end of tile t waits for tile t+1 (later tiles' transfers
+        // may still be pending), joins the barrier after which no wave reads
+        // stage t % NSK any more, and sends tile t+NSK there.
+        auto wait_tiles = [&](int n) FA2_INLINE {   // at most n tiles' transfers pending
+            if (n <= 0) vm_wait<0>();
+            else if (n == 1) vm_wait<TPT>();
+            else vm_wait<2 * TPT>();
+        };
+        if (NSK - 1 < ntiles) issue_next();   // the last stage's tile (the prologue sent the others)
+        wait_tiles(min(NSK - 1, ntiles - 1));
+        lds_barrier();                         // tile 0 landed for every wave
+        for (int t = 0; t < ntiles; ++t) {
+            if (t <= tlast) {
+                const int st = stage_of(t);
+                const bool m = need_mask(t);
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    if (!DROPOUT) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) dpA[r] = -dl[0];
+                    }
+#pragma unroll
+                    for (int sti = 0; sti < 4; ++sti) {
+                        const h8 ka = rrow(st, 0, kb, sti), va = rrow(st, 1, kb, sti);
+                        sA = sti == 0 ? mfma32_first(ka, qf[0][0]) : mfma32(ka, qf[0][sti], sA);
+                        dpA = (sti == 0 && DROPOUT) ? mfma32_first(va, dof[0][0]) : mfma32(va, dof[0][sti], dpA);
+                    }
+                    if (m) {
+                        FA2_COLD_BRANCH();
+                        mask(t, kb, 0, sA);
+                    }
+                    ds_form(t, kb, 0, sA, dpA, dsA);
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int db = 0; db < 2; ++db) dq[0][db] = mfma32(trk(st, kb, db, hh), dsA[hh], dq[0][db]);
+                }
+            }
+            if (t + 1 < ntiles) {
+                wait_tiles(min(NSK - 2, ntiles - 2 - t));   // tile t+1 landed
+                lds_barrier();
+                if (t + NSK < ntiles) issue_next();
+            }
+        }
+        vm_wait<0>();
+        lds_barrier();   // every wave is done with the stages: the dQ staging reuses them
+    } else {
+        // Two query blocks: S and dP of both from one pass over the K / V row
+        // fragments (each fragment read from LDS feeds two MFMAs), dS, then dQ
+        // of both from one pass over the K^T fragments.
         // Tiles are computed in pairs with one barrier after each pair: while
         // tiles t-1, t are read, t+1, t+2 are in flight; the pair's end waits
         // for those two (every issued transfer) and refills the two stages
         // just read with tiles t+3, t+4.  Tile 3 goes out now.
-        constexpr int TPT = DMASK ? 6 : 4;   // transfers per tile and wave
-        if (QP_NST - 1 < ntiles) issue_next();
+        if (NSK - 1 < ntiles) issue_next();
         auto wait_pending = [&](int n) FA2_INLINE {
             if (n <= 0) vm_wait<0>();
             else if (n == 1) vm_wait<TPT>();
             else if (n == 2) vm_wait<2 * TPT>();
             else vm_wait<3 * TPT>();
         };
-        wait_pending(min(QP_NST - 2, ntiles - 2));   // tiles 0 and 1 landed
+        wait_pending(min(NSK - 2, ntiles - 2));   // tiles 0 and 1 landed
         lds_barrier();
         for (int t = 0; t < ntiles; ++t) {
             const int st = stage_of(t);
@@ -325,31 +393,32 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             dpA[r] = -dl[0];
-                            dpB[r] = -dl[1];
+                            dpB[r] = -dl[QB - 1];
                         }
                     }
 #pragma unroll
                     for (int sti = 0; sti < 4; ++sti) {
                         const h8 ka = rrow(st, 0, kb, sti), va = rrow(st, 1, kb, sti);
                         sA = sti == 0 ? mfma32_first(ka, qf[0][0]) : mfma32(ka, qf[0][sti], sA);
-                        sB = sti == 0 ? mfma32_first(ka, qf[1][0]) : mfma32(ka, qf[1][sti], sB);
+                        sB = sti == 0 ? mfma32_first(ka, qf[QB - 1][0]) : mfma32(ka, qf[QB - 1][sti], sB);
                         dpA = (sti == 0 && DROPOUT) ? mfma32_first(va, dof[0][0]) : mfma32(va, dof[0][sti], dpA);
-                        dpB = (sti == 0 && DROPOUT) ? mfma32_first(va, dof[1][0]) : mfma32(va, dof[1][sti], dpB);
+                        dpB = (sti == 0 && DROPOUT) ? mfma32_first(va, dof[QB - 1][0])
+                                                    : mfma32(va, dof[QB - 1][sti], dpB);
                     }
                     if (m) {
                         FA2_COLD_BRANCH();
                         mask(t, kb, 0, sA);
-                        mask(t, kb, 1, sB);
+                        mask(t, kb, QB - 1, sB);
                     }
                     ds_form(t, kb, 0, sA, dpA, dsA);
-                    ds_form(t, kb, 1, sB, dpB, dsB);
+                    ds_form(t, kb, QB - 1, sB, dpB, dsB);
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                         for (int db = 0; db < 2; ++db) {
                             const h8 kt = trk(st, kb, db, hh);
                             dq[0][db] = mfma32(kt, dsA[hh], dq[0][db]);
-                            dq[1][db] = mfma32(kt, dsB[hh], dq[1][db]);
+                            dq[QB - 1][db] = mfma32(kt, dsB[hh], dq[QB - 1][db]);
                         }
                 }
             }
@@ -362,18 +431,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_pipe_kernel(const BwdArgs a) {
         }
     }
 
-    // dQ rows leave through LDS (store_rows_f16).  The last pair (or single
-    // last tile) has no barrier after it, so other waves may still read the
-    // stages of tiles ntiles-2 and ntiles-1; stages ntiles % 4 and
-    // (ntiles + 1) % 4 are idle (their last reads precede an earlier barrier,
-    // no later transfer refilled them, and every transfer has landed): waves
-    // 0, 1 use the first, waves 2, 3 the second, 4 KB per 32-query block.
-    static_assert(QP_NST == 4 && DQ_QB == 2 && sizeof(sKV[0]) == 16384, "dQ staging layout");
+    // dQ rows leave through LDS (store_rows_f16), 4 KB per 32-query block.
+    // NARROW: after the final barrier every stage is idle; wave w uses
+    // bytes 4096*w on.  Otherwise the last pair (or single last tile) has no
+    // barrier after it, so other waves may still read the stages of tiles
+    // ntiles-2 and ntiles-1; stages ntiles % 4 and (ntiles + 1) % 4 are idle
+    // (their last reads precede an earlier barrier, no later transfer
+    // refilled them, and every transfer has landed): waves 0, 1 use the
+    // first, waves 2, 3 the second.
+    static_assert(NARROW ? sizeof(sKV) >= DQ_NW * 4096 : (NSK == 4 && QB == 2 && sizeof(sKV[0]) == 16384),
+                  "dQ staging layout");
     const float sc = a.scale;
     const bool dq16 = ((a.dqsb | a.dqsh | a.dqss) & 7) == 0;
-    char *const stg = reinterpret_cast<char *>(sKV[stage_of(ntiles + (wave >> 1))]) + 8192 * (wave & 1);
+    char *const stg = NARROW ? reinterpret_cast<char *>(&sKV[0][0][0]) + 4096 * wave
+                             : reinterpret_cast<char *>(sKV[stage_of(ntiles + (wave >> 1))]) + 8192 * (wave & 1);
 #pragma unroll
-    for (int qb = 0; qb < DQ_QB; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
         store_rows_f16(dq[qb][0], dq[qb][1], sc, stg + 4096 * qb, dQp + (int64_t)(qw0 + 32 * qb) * a.dqss, a.dqss,
                        S - (qw0 + 32 * qb), dq16);
 }
@@ -862,25 +935,43 @@ hipError_t launch_bwd_delta(const BwdArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
-    const int nqblk = (a.S + DQ_QWG - 1) / DQ_QWG;
-    const dim3 grid((unsigned)(nqblk * a.B * a.H)), block(256);
+// Sequences up to this length take the narrow dQ kernel (one query block per
+// wave, three waves per SIMD); longer ones the two-block kernel, whose shared
+// K / V fragments halve the LDS reads per MFMA.  Measured at B*S = 32k, H = 12:
+// S = 512 7% faster narrow, S = 1024 2.5% faster, S = 4096 6.5% slower.
+#ifndef FA2_DQ_NARROW_MAX_S
+#define FA2_DQ_NARROW_MAX_S 1024
+#endif
+
+// Keep-bit words always take the two-block kernel: reading them, the narrow
+// one needs more registers than three waves per SIMD leave.
+template <bool NARROW>
+static void launch_dq_t(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    const int qwg = NARROW && !(dropout && a.drop_mask != nullptr) ? DQ_NW * 32 : DQ_QWG;
+    const dim3 grid((unsigned)((a.S + qwg - 1) / qwg * a.B * a.H)), block(256);
     const bool dmask = dropout && a.drop_mask != nullptr;
     if (causal) {
         if (dmask)
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true, true, false>), grid, block, 0, st, a);
         else if (dropout)
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, true, false, NARROW>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<true, false, false, NARROW>), grid, block, 0, st, a);
     } else {
         if (dmask)
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true, true>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true, true, false>), grid, block, 0, st, a);
         else if (dropout)
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, true, false, NARROW>), grid, block, 0, st, a);
         else
-            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, false, false>), grid, block, 0, st, a);
+            hipLaunchKernelGGL((bwd_dq_pipe_kernel<false, false, false, NARROW>), grid, block, 0, st, a);
     }
+}
+
+hipError_t launch_bwd_dq(const BwdArgs &a, bool causal, bool dropout, hipStream_t st) {
+    if (a.S <= FA2_DQ_NARROW_MAX_S)
+        launch_dq_t<true>(a, causal, dropout, st);
+    else
+        launch_dq_t<false>(a, causal, dropout, st);
     return hipGetLastError();
 }
 

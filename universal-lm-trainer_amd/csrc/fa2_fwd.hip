@@ -74,17 +74,33 @@ constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <
 //
 // DMASK (dropout, no key slices): each lane also stores its tile's 32 keep
 // bits as one word of a.drop_mask (dmask_word layout), for the backward.
-template <bool CAUSAL, bool DROPOUT, bool SPLIT, bool DMASK, int QBT>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
+//
+// NARROW (one query block per wave): the in-order loop with three LDS stages
+// and one barrier per tile, at most 168 registers per lane, so that three
+// workgroups (three waves per SIMD) share a CU: with one query block a wave's
+// scores -> softmax -> P V chain is short, and a third wave covers its
+// latencies.
+#ifndef FA2_FWD_NARROW_WAVES
+#define FA2_FWD_NARROW_WAVES 4
+#endif
+constexpr int NARROW_WAVES = FA2_FWD_NARROW_WAVES;   // waves per SIMD of the narrow loop: 3 or 4
+static_assert(NARROW_WAVES == 3 || NARROW_WAVES == 4, "three or four narrow waves per SIMD");
+
+template <bool CAUSAL, bool DROPOUT, bool SPLIT, bool DMASK, int QBT, bool NARROW = false>
+__global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_kernel(const FwdArgs a) {
     constexpr int QB = QBT;
     constexpr int QWG = qwg_of(QBT);
-    constexpr bool NOPIPE = QBT == 2;
+    constexpr bool NOPIPE = QBT == 2 || NARROW;
+    // LDS stages of this variant (narrow: 48 KB or 32 KB per workgroup, so
+    // that three or four workgroups fit the CU's 160 KB).
+    constexpr int NSK = NARROW ? (NARROW_WAVES == 4 ? 2 : 3) : NST;
     static_assert(QBT == 1 || QBT == 2, "one or two query blocks per wave");
-    static_assert(!DMASK || (DROPOUT && !SPLIT && NST == 4), "keep-bit words: the unsplit forward");
-    static_assert(!(DMASK && QBT == 2), "keep-bit words: the one-block (pipelined) loop");
-    static_assert(!NOPIPE || NST == 4, "the unpipelined loop's waits assume four stages");
-    // NST stages of one K tile and one V tile (8 KB each, swizzled chunks).
-    __shared__ __attribute__((aligned(16))) h8 sKV[NST][2][KT * 8];
+    static_assert(!NARROW || QBT == 1, "the narrow loop holds one query block per wave");
+    static_assert(!DMASK || (DROPOUT && !SPLIT && (NARROW || NST == 4)), "keep-bit words: the unsplit forward");
+    static_assert(!(DMASK && QBT == 2), "keep-bit words: the one-block loops");
+    static_assert(!NOPIPE || NARROW || NST == 4, "the unpipelined loop's waits assume four stages");
+    // NSK stages of one K tile and one V tile (8 KB each, swizzled chunks).
+    __shared__ __attribute__((aligned(16))) h8 sKV[NSK][2][KT * 8];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
@@ -148,11 +164,16 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // key row k0 + row.  The lane's byte offsets within a tile are fixed; only
     // the last tile, whose rows past Sk are redirected to row Sk - 1 (any
     // finite row: their scores are masked and their P is zero), needs them
-    // recomputed.
-    const int lrow = lane >> 3;
-    const int kch[2] = {(lane & 7) ^ swz_rows(lrow), (lane & 7) ^ swz_rows(lrow + 8)};
-    const int vch = (lane & 7) ^ swz_tr(lrow);
+    // recomputed.  The narrow variant recomputes them for every tile from the
+    // lane index, re-read through an opaque move so that nothing derived from
+    // it stays live across the tile loop: a few VALU operations per tile save
+    // the registers that let four waves share a SIMD.
     auto tile_offsets = [&](int k0, uint32_t(&ko)[2], uint32_t(&vo)[2]) FA2_INLINE {
+        int ln = lane;
+        if (NARROW) asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+        const int lrow = ln >> 3;
+        const int kch[2] = {(ln & 7) ^ swz_rows(lrow), (ln & 7) ^ swz_rows(lrow + 8)};
+        const int vch = (ln & 7) ^ swz_tr(lrow);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
             const int row = min(k0 + 8 * (TPW * wave + i) + lrow, Sk - 1) - k0;
@@ -161,9 +182,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         }
     };
     // Stage of tile t (t >= 0; unsigned, so a power-of-two count is a mask).
-    auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)NST); };
-    uint32_t koffg[2], voffg[2];
-    tile_offsets(0, koffg, voffg);
+    auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)NSK); };
+    uint32_t koffg[2] = {0u, 0u}, voffg[2] = {0u, 0u};
+    if (!NARROW) tile_offsets(0, koffg, voffg);
     // Tiles are issued in order, once each: issue_next() sends the next tile
     // (the callers' index tests only decide whether there is one).  Scalar
     // running addresses (global tile bases, LDS stage) advance by a constant
@@ -177,7 +198,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 1024u * (uint32_t)(TPW * wave);
     auto issue_next = [&]() FA2_INLINE {
         uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
-        if (kn + KT > Sk) tile_offsets(kn, ko, vo);
+        if (NARROW || kn + KT > Sk) tile_offsets(kn, ko, vo);
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
             const uint32_t d = lds_kv + stn * (uint32_t)sizeof(sKV[0]) + 1024u * (uint32_t)i;
@@ -187,10 +208,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         gk += k_step;
         gv += v_step;
         kn += KT;
-        stn = (stn + 1 == NST) ? 0 : stn + 1;
+        stn = (stn + 1 == NSK) ? 0 : stn + 1;
     };
 #pragma unroll
-    for (int t = 0; t < NST - 1; ++t)
+    for (int t = 0; t < NSK - 1; ++t)
         if (t < ntiles) issue_next();
 
     f16x o[QB][2];                      // O^T, d blocks 0..31 and 32..63
@@ -450,7 +471,86 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
     // are in flight.  The barrier after step t publishes tile t+2 and frees
     // the stage of tile t-1 for tile t+NST-1.
     static_assert(NST == 4 || NST == 5, "three resident tiles plus one or two in flight");
-    if constexpr (NOPIPE) {
+    // One tile of the in-order loops: scores, masking, softmax (with its cold
+    // path on the live scores), dropout, P V; returns the keep word of query
+    // block 0 (DMASK).
+    auto inorder_tile = [&](int t, f16x(&s)[QB][2], h8(&p)[QB][2][2]) FA2_INLINE -> uint32_t {
+        const int k0 = kbase + t * KT;
+        const int stage = stage_of(t);
+        uint32_t w = 0;
+        s_mm(stage, s);
+        if (need_mask(k0)) {
+            FA2_COLD_BRANCH();
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) mask(qb, k0, s[qb]);
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            float rs = p_form(s[qb], msc[qb], p[qb]);
+            if (__any(!(rs <= P_SUM_LIMIT))) {
+                // The cold path on the live scores: true row max, rescale of
+                // O and l, P again (on the first tile msc is -inf and it
+                // always runs).
+                FA2_COLD_BRANCH();
+                float mx = s[qb][0][0];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
+                mx = fmaxf(mx, xor32(mx));
+                const float mnew = fmaxf(msc[qb], mx * scale2);
+                const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc[qb] - mnew);
+                msc[qb] = mnew;
+                l[qb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+                rs = p_form(s[qb], (mnew == -INFINITY) ? 0.f : mnew, p[qb]);
+            }
+            l[qb] += rs;
+            if (DROPOUT) {
+                const uint32_t wq = drop_apply(qb, k0, p[qb]);
+                if (qb == 0) w = wq;
+            }
+        }
+        pv(stage, p);
+        return w;
+    };
+    if constexpr (NARROW) {
+        // NSK stages: tile t is read while tiles t+1 .. t+NSK-1 are in
+        // flight.  The end of tile t waits for tile t+1 (the transfers of
+        // tiles t+2 .. t+NSK-1 may still be pending), joins the barrier
+        // after which no wave reads stage t % NSK any more, and sends tile
+        // t+NSK there.  DMASK: the tile's keep word is stored after that
+        // wait; a store still in flight at the next wait only makes its count
+        // stricter (the loads complete in order), so the waits stay exact.
+        auto wait_tiles = [&](int n) FA2_INLINE {   // at most n tiles' transfers pending
+            if (n <= 0) vm_wait<0>();
+            else if (n == 1) vm_wait<2 * TPW>();
+            else vm_wait<4 * TPW>();
+        };
+        if (NSK - 1 < ntiles) issue_next();   // the last stage's tile (the prologue sent the others)
+        wait_tiles(min(NSK - 1, ntiles - 1));
+        lds_barrier();                         // tile 0 landed for every wave
+        f16x s[QB][2];
+        h8 p[QB][2][2];
+        for (int t = 0; t < ntiles; ++t) {
+            uint32_t w = 0;
+            if (t <= tlast) w = inorder_tile(t, s, p);
+            if (t + 1 < ntiles) {
+                wait_tiles(min(NSK - 2, ntiles - 2 - t));   // tile t+1 landed
+                lds_barrier();
+                if (t + NSK < ntiles) issue_next();
+            }
+            if (DMASK && t <= tlast) {
+                const int q = qw0 + c;   // QB == 1
+                if (q < S) a.drop_mask[dmask_word(CAUSAL, bh, S, kbase / KT + t, g2, q)] = w;
+            }
+        }
+        vm_wait<0>();
+        lds_barrier();   // every wave is done with the stages: the epilogue reuses them
+    } else if constexpr (NOPIPE) {
         // Tiles are computed in pairs with one barrier after each pair: while
         // tiles t-1, t are read, t+1, t+2 are in flight; the pair's end waits
         // for those two (every issued transfer) and refills the two stages
@@ -467,44 +567,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_kernel(const FwdArgs a) {
         f16x s[QB][2];
         h8 p[QB][2][2];
         for (int t = 0; t < ntiles; ++t) {
-            const int k0 = kbase + t * KT;
-            const int stage = stage_of(t);
-            if (t <= tlast) {
-                s_mm(stage, s);
-                if (need_mask(k0)) {
-                    FA2_COLD_BRANCH();
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb) mask(qb, k0, s[qb]);
-                }
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    float rs = p_form(s[qb], msc[qb], p[qb]);
-                    if (__any(!(rs <= P_SUM_LIMIT))) {
-                        // The cold path on the live scores: true row max,
-                        // rescale of O and l, P again (on the first tile msc
-                        // is -inf and it always runs).
-                        FA2_COLD_BRANCH();
-                        float mx = s[qb][0][0];
-#pragma unroll
-                        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
-                        mx = fmaxf(mx, xor32(mx));
-                        const float mnew = fmaxf(msc[qb], mx * scale2);
-                        const float alpha = (mnew == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(msc[qb] - mnew);
-                        msc[qb] = mnew;
-                        l[qb] *= alpha;
-#pragma unroll
-                        for (int db = 0; db < 2; ++db)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
-                        rs = p_form(s[qb], (mnew == -INFINITY) ? 0.f : mnew, p[qb]);
-                    }
-                    l[qb] += rs;
-                    if (DROPOUT) (void)drop_apply(qb, k0, p[qb]);
-                }
-                pv(stage, p);
-            }
+            if (t <= tlast) (void)inorder_tile(t, s, p);
             if (!(t & 1) && t + 1 < ntiles) continue;   // the pair's first tile
             vm_wait<0>();                                // tiles t+1, t+2 (the next pair) landed
             lds_barrier();                               // every wave is done with tiles t-1, t
@@ -859,11 +922,34 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_kernel(const FwdArgs a) {
     if (lane == 0) a.lse[b * a.lsb + h * a.lsh] = (M == -INFINITY || !(L > 0.f)) ? -INFINITY : (M + log2f(L)) * LN2;
 }
 
+#ifndef FA2_FWD_NARROW
+#define FA2_FWD_NARROW 1
+#endif
+
+template <bool CAUSAL, bool DROPOUT, bool DMASK>
+void launch_narrow(const FwdArgs &a, hipStream_t st) {
+    const int nqblk = (a.S + qwg_of(1) - 1) / qwg_of(1);
+    hipLaunchKernelGGL((fwd_kernel<CAUSAL, DROPOUT, false, DMASK, 1, true>), dim3((unsigned)(nqblk * a.B * a.H)),
+                       dim3(NW * 64), 0, st, a);
+}
+
 template <bool SPLIT>
 void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const dim3 block(NW * 64);
     // Keep-bit words only from the unsplit forward (the training path).
     const bool dmask = !SPLIT && dropout && a.drop_mask != nullptr;
+    if (!SPLIT && FA2_FWD_NARROW) {
+        if (causal) {
+            if (dmask) launch_narrow<true, true, true>(a, st);
+            else if (dropout) launch_narrow<true, true, false>(a, st);
+            else launch_narrow<true, false, false>(a, st);
+        } else {
+            if (dmask) launch_narrow<false, true, true>(a, st);
+            else if (dropout) launch_narrow<false, true, false>(a, st);
+            else launch_narrow<false, false, false>(a, st);
+        }
+        return;
+    }
     // Without key slices or keep-bit words: two query blocks per wave (2 to 3%
     // faster than the pipelined single block) when that still fills every
     // slot of two workgroups per CU; otherwise (short query ranges: prefill
