@@ -938,7 +938,15 @@ void launch_fwd_t(const FwdArgs &a, bool causal, bool dropout, hipStream_t st) {
     const dim3 block(NW * 64);
     // Keep-bit words only from the unsplit forward (the training path).
     const bool dmask = !SPLIT && dropout && a.drop_mask != nullptr;
-    if (!SPLIT && FA2_FWD_NARROW) {
+    // The narrow kernel (one query block per wave, four workgroups per CU)
+    // when its grid fills at least one round of those slots: the training
+    // shapes (measured at B*S = 32k: 7% faster at S = 4096, 20% at S = 512)
+    // and large prefill chunks.  Smaller grids -- prefill chunks of a few
+    // hundred queries over long caches, where every workgroup runs the whole
+    // key range -- keep the software-pipelined kernel below (the narrow one
+    // was 5-16% slower there).
+    const int64_t narrow_wgs = (int64_t)((a.S + qwg_of(1) - 1) / qwg_of(1)) * a.B * a.H;
+    if (!SPLIT && FA2_FWD_NARROW && narrow_wgs >= (int64_t)NARROW_WAVES * device_cus()) {
         if (causal) {
             if (dmask) launch_narrow<true, true, true>(a, st);
             else if (dropout) launch_narrow<true, true, false>(a, st);
