@@ -256,18 +256,28 @@ def cpu_baseline():
 def rope_timing(torch, ext, B, H, S, stream, n=20):
     """Fused RoPE (rope_fwd / rope_bwd) at the configuration's shape on q, k
     views of a fused qkv tensor, as train.py hands them over
-    (reference @ None: train.py:1909-1913): mean of n calls between HIP events,
-    and the rate of its compulsory HBM bytes (q, k read and written, cos and
-    sin rows read) against 8 TB/s."""
+    (reference @ None: train.py:1909-1913), and the rate of its compulsory HBM
+    bytes (q, k read and written, cos and sin rows read) against 8 TB/s:
+      * `us`: the kernel, launched through the C ABI (fa2_rope_f16) into
+        preallocated outputs, mean of n launches between HIP events on the
+        launch stream;
+      * `binding_call_us`: the same through the torch binding, which allocates
+        its two outputs on every call (host time included when the host falls
+        behind)."""
+    import ctypes as ct
+    import fa2_capi
     import fa2_workloads as wl
+    lib = fa2_capi.load()
     qkv = torch.randn(B, S, 3 * H * 64, device="cuda", dtype=torch.float16)
     q, k, _ = (t.view(B, S, H, 64).transpose(1, 2) for t in qkv.chunk(3, dim=-1))
     cos, sin = (t.cuda() for t in wl.rope_tables(S))
+    qo = torch.empty(B, S, H, 64, device="cuda", dtype=torch.float16).transpose(1, 2)
+    ko = torch.empty_like(qo)
+    pr = fa2_capi.rope_params(q, k, qo, ko, cos, sin)
+    sp = ct.c_void_p(stream.cuda_stream)
     nbytes = 4 * B * H * S * 64 * 2 + 2 * S * 64 * 4
-    out = {}
-    for name in ("fwd", "bwd"):
-        call = (lambda: ext.rope_fwd(q, k, cos, sin)) if name == "fwd" else \
-               (lambda: ext.rope_bwd(q, k, cos, sin, q, k))
+
+    def events(call):
         for _ in range(3):
             call()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -276,9 +286,15 @@ def rope_timing(torch, ext, B, H, S, stream, n=20):
             call()
         e1.record(stream)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / n * 1e3
+        return e0.elapsed_time(e1) / n * 1e3
+
+    out = {}
+    for name, bwd in (("fwd", 0), ("bwd", 1)):
+        us = events(lambda: lib.fa2_rope_f16(ct.byref(pr), bwd, sp))
+        bind = events((lambda: ext.rope_fwd(q, k, cos, sin)) if not bwd else (lambda: ext.rope_bwd(q, k, cos, sin, q, k)))
         gbs = nbytes / (us / 1e6) / 1e9
-        out[name] = {"us": round(us, 2), "gb_s": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_GBS, 4)}
+        out[name] = {"us": round(us, 2), "gb_s": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_GBS, 4),
+                     "binding_call_us": round(bind, 2)}
     out["bytes_per_call"] = nbytes
     return out
 
@@ -424,7 +440,7 @@ def decoder_step(args, torch, fa):
                  "attention_ms_per_step": round(attn_ms, 3),
                  "attention_share": round(attn_ms / ms_per_step, 4),
                  "approx_model_tflops": round(dec.approx_step_flops(B, S) / (ms_per_step / 1e3) / 1e12, 1),
-                 "last_loss": round(float(loss), 4)},
+                 "last_loss": round(float(loss.detach()), 4)},
         "clock": clock,
         "parity": parity,
     }

@@ -137,3 +137,13 @@ def bwd_params(q, k, v, o, lse, do, dq, dk, dv, scale, causal=True, dropout_p=0.
     p.B, p.H, p.S, p.D = q.size(0), q.size(1), q.size(2), q.size(3)
     p.softmax_scale, p.dropout_p, p.seed, p.causal = scale, dropout_p, seed, int(causal)
     return p
+
+
+def rope_params(q, k, qo, ko, cos, sin):
+    p = RopeParams()
+    p.q, p.k, p.qo, p.ko = q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr()
+    p.cos, p.sin = cos.data_ptr(), sin.data_ptr()
+    p.q_stride, p.k_stride, p.qo_stride, p.ko_stride = strides3(q), strides3(k), strides3(qo), strides3(ko)
+    p.cs_stride, p.sn_stride = cos.stride(0), sin.stride(0)
+    p.B, p.H, p.S, p.D = q.size(0), q.size(1), q.size(2), q.size(3)
+    return p
