@@ -342,14 +342,18 @@ __device__ __forceinline__ uint32_t dropout_row_part(uint32_t seed, int row, uin
 __device__ __forceinline__ uint32_t dropout_col_part(uint32_t seed, int col, uint32_t bh) {
     return (seed * 0x9E3779B1u) ^ dropout_col_term(col) ^ ((bh + 1u) * 0x27D4EB2Fu);
 }
-// Keep decision from the full hash input x.
-__device__ __forceinline__ bool dropout_keep_hashed(uint32_t x, uint32_t thr) {
+// The finaliser (lowbias32) of the full hash input x.
+__device__ __forceinline__ uint32_t dropout_mix(uint32_t x) {
     x ^= x >> 16;
     x *= 0x7feb352du;
     x ^= x >> 15;
     x *= 0x846ca68bu;
     x ^= x >> 16;
-    return x >= (thr << 8);
+    return x;
+}
+// Keep decision from the full hash input x.
+__device__ __forceinline__ bool dropout_keep_hashed(uint32_t x, uint32_t thr) {
+    return dropout_mix(x) >= (thr << 8);
 }
 __device__ __forceinline__ bool dropout_keep(uint32_t seed, int row, int col, uint32_t bh,
                                              uint32_t thr) {

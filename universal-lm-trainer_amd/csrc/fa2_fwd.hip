@@ -333,18 +333,15 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     // Dropout on the P of query block qb, tile k0 (l already holds its
     // un-dropped sum); returns the keep word (DMASK) of the lane's query.
     auto drop_apply = [&](int qb, int k0, h8(&pb)[2][2]) FA2_INLINE -> uint32_t {
-        // l sums the un-dropped P; dropout then zeroes / rescales P.
-        // The keep decision selects the multiplier m = -1/(1-p) or +0, and
-        // each packed fp16 pair of P is scaled in place by two mixed-
-        // precision FMAs, v_fma_mixlo_f16 / v_fma_mixhi_f16: (-P) * m + 0
-        // in fp32 with P read as fp16 (op_sel_hi bit 1 of source 0; op_sel
-        // bit 1 picks its high half; "-" negates it) and m as fp32, the
-        // result rounded to fp16 into the low / high half.  That is one
-        // instruction per element instead of a widen, a multiply and half
-        // a repack.  m's sign bit is the keep bit: DMASK shifts it into
-        // the word (one funnel shift, v_alignbit_b32, per element), so
+        // l sums the un-dropped P; dropout then zeroes the dropped elements
+        // of P in place (the 1/(1-p) of the kept ones scales O once, in the
+        // epilogue).  Per element: the keep compare into VCC, then an SDWA
+        // v_cndmask that rewrites the element's 16-bit half of the packed
+        // pair with itself or 0 and preserves the other half.  DMASK: the
+        // same VCC bit enters the word by v_addc_co (w = 2w + keep), so
         // element 16*kb + 8*hh + e lands on bit 31 - (16*kb + 8*hh + e).
         uint32_t w = 0;
+        const uint32_t hthr = a.drop_thr << 8;
         const uint32_t hrow = dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -354,20 +351,35 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
                 u4x pk = __builtin_bit_cast(u4x, pb[kb][hh]);
 #pragma unroll
                 for (int e2 = 0; e2 < 4; ++e2) {
-                    float m[2];
+                    uint32_t r = pk[e2];
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
                         const int e = 2 * e2 + j;
                         const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
-                        const bool keep = dropout_keep_hashed(hrow ^ dropout_col_term(key), a.drop_thr);
-                        m[j] = keep ? -a.inv_keep : 0.f;
-                        if (DMASK) w = (w << 1) | (__builtin_bit_cast(uint32_t, m[j]) >> 31);
+                        const uint32_t h = dropout_mix(hrow ^ dropout_col_term(key));
+                        if (j == 0 && DMASK)
+                            asm("v_cmp_le_u32 vcc, %3, %2\n\t"
+                                "v_cndmask_b32_sdwa %0, 0, %0, vcc dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE "
+                                "src0_sel:WORD_0 src1_sel:WORD_0\n\t"
+                                "v_addc_co_u32 %1, vcc, %1, %1, vcc"
+                                : "+v"(r), "+v"(w) : "v"(h), "s"(hthr) : "vcc");
+                        else if (DMASK)
+                            asm("v_cmp_le_u32 vcc, %3, %2\n\t"
+                                "v_cndmask_b32_sdwa %0, 0, %0, vcc dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE "
+                                "src0_sel:WORD_1 src1_sel:WORD_1\n\t"
+                                "v_addc_co_u32 %1, vcc, %1, %1, vcc"
+                                : "+v"(r), "+v"(w) : "v"(h), "s"(hthr) : "vcc");
+                        else if (j == 0)
+                            asm("v_cmp_le_u32 vcc, %2, %1\n\t"
+                                "v_cndmask_b32_sdwa %0, 0, %0, vcc dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE "
+                                "src0_sel:WORD_0 src1_sel:WORD_0"
+                                : "+v"(r) : "v"(h), "s"(hthr) : "vcc");
+                        else
+                            asm("v_cmp_le_u32 vcc, %2, %1\n\t"
+                                "v_cndmask_b32_sdwa %0, 0, %0, vcc dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE "
+                                "src0_sel:WORD_1 src1_sel:WORD_1"
+                                : "+v"(r) : "v"(h), "s"(hthr) : "vcc");
                     }
-                    uint32_t r;
-                    asm("v_fma_mixlo_f16 %0, -%1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pk[e2]), "v"(m[0]));
-                    asm("v_fma_mixhi_f16 %0, -%1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-                        : "+v"(r)
-                        : "v"(pk[e2]), "v"(m[1]));
                     pk[e2] = r;
                 }
                 pb[kb][hh] = __builtin_bit_cast(h8, pk);
@@ -733,7 +745,9 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
         const float lt = l[qb] + xor32(l[qb]);
         const int q = qw0 + 32 * qb + c;
         if (q < S && g2 == 0) Lp[q] = (msc[qb] == -INFINITY) ? -INFINITY : (msc[qb] + log2f(lt)) * LN2;
-        store_rows_f16(o[qb][0], o[qb][1], lt > 0.f ? 1.f / lt : 0.f, stage_base + 4096 * (QB * wave + qb),
+        // With dropout, P was zeroed but not scaled: 1/(1-p) joins 1/l here.
+        const float oscale = lt > 0.f ? (DROPOUT ? a.inv_keep / lt : 1.f / lt) : 0.f;
+        store_rows_f16(o[qb][0], o[qb][1], oscale, stage_base + 4096 * (QB * wave + qb),
                        Op + (int64_t)(qw0 + 32 * qb) * a.oss, a.oss, S - (qw0 + 32 * qb), o16);
     }
 }
@@ -765,7 +779,8 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdArgs a) {
             for (int j = 0; j < 4; ++j) acc[j] += w * x[j];
         }
     }
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    // inv_keep: 1/(1-p), which the slices left out of their O (1 without dropout).
+    const float inv = lsum > 0.f ? a.inv_keep / lsum : 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] *= inv;
     *reinterpret_cast<h4 *>(a.o + b * a.osb + h * a.osh + (int64_t)q * a.oss + 4 * part) =
