@@ -351,6 +351,22 @@ __device__ __forceinline__ uint32_t dropout_mix(uint32_t x) {
     x ^= x >> 16;
     return x;
 }
+// The finaliser split for callers that share the column part between lanes.
+// Its first step distributes over the xor of the two parts:
+//   x ^ (x >> 16) = (r ^ (r >> 16)) ^ (k ^ (k >> 16))   for x = r ^ k,
+// so dropout_xs16 of the row part and of the column term can be formed apart.
+// Its last step folds into the keep compare: with T = thr << 8 and x4 the
+// value before x4 ^ (x4 >> 16),
+//   x4 ^ (x4 >> 16) >= T   <=>   (x4 ^ (T >> 16)) >= T,
+// since both sides have the high half of x4 and, where that equals T's high
+// half, the same low half.  dropout_mix_tail returns x4 ^ (T >> 16).
+__device__ __forceinline__ uint32_t dropout_xs16(uint32_t v) { return v ^ (v >> 16); }
+__device__ __forceinline__ uint32_t dropout_mix_tail(uint32_t x1, uint32_t thi) {
+    x1 *= 0x7feb352du;
+    x1 ^= x1 >> 15;
+    x1 *= 0x846ca68bu;
+    return x1 ^ thi;
+}
 // Keep decision from the full hash input x.
 __device__ __forceinline__ bool dropout_keep_hashed(uint32_t x, uint32_t thr) {
     return dropout_mix(x) >= (thr << 8);

@@ -101,6 +101,9 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     static_assert(!NOPIPE || NARROW || NST == 4, "the unpipelined loop's waits assume four stages");
     // NSK stages of one K tile and one V tile (8 KB each, swizzled chunks).
     __shared__ __attribute__((aligned(16))) h8 sKV[NSK][2][KT * 8];
+    // Dropout: per wave, the column part dropout_xs16(col term) of the
+    // current tile's KT keys, formed once per key and read by every lane.
+    __shared__ __attribute__((aligned(16))) uint32_t sDK[DROPOUT ? NW * KT : 1];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
@@ -335,28 +338,37 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     auto drop_apply = [&](int qb, int k0, h8(&pb)[2][2]) FA2_INLINE -> uint32_t {
         // l sums the un-dropped P; dropout then zeroes the dropped elements
         // of P in place (the 1/(1-p) of the kept ones scales O once, in the
-        // epilogue).  Per element: the keep compare into VCC, then an SDWA
-        // v_cndmask that rewrites the element's 16-bit half of the packed
-        // pair with itself or 0 and preserves the other half.  DMASK: the
-        // same VCC bit enters the word by v_addc_co (w = 2w + keep), so
-        // element 16*kb + 8*hh + e lands on bit 31 - (16*kb + 8*hh + e).
+        // epilogue).  The hash of element (query, key) is the finaliser of
+        // row part ^ column term, taken apart as dropout_xs16 of each part
+        // (the column parts of the tile's 64 keys one per lane, through this
+        // wave's LDS slot: the wave's own stores precede its reads, in
+        // order) and dropout_mix_tail, compared with T = thr << 8.  Per
+        // element: the compare into VCC, then an SDWA v_cndmask that
+        // rewrites the element's 16-bit half of the packed pair with itself
+        // or 0 and preserves the other half.  DMASK: the same VCC bit enters
+        // the word by v_addc_co (w = 2w + keep), so element 16*kb + 8*hh + e
+        // lands on bit 31 - (16*kb + 8*hh + e).
+        uint32_t *const kpart = &sDK[DROPOUT ? KT * wave : 0];
+        kpart[lane] = dropout_xs16(dropout_col_term(k0 + lane));
         uint32_t w = 0;
-        const uint32_t hthr = a.drop_thr << 8;
-        const uint32_t hrow = dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh);
+        const uint32_t hthr = a.drop_thr << 8, thi = hthr >> 16;
+        const uint32_t rpart = dropout_xs16(dropout_row_part(a.seed, qw0 + 32 * qb + c, (uint32_t)bh));
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 typedef uint32_t u4x __attribute__((ext_vector_type(4)));
                 u4x pk = __builtin_bit_cast(u4x, pb[kb][hh]);
+                // keys 32*kb + 16*hh + 8*m + 4*g2 + (0..3) of the tile
+                const u4x kp0 = *reinterpret_cast<const u4x *>(&kpart[32 * kb + 16 * hh + 4 * g2]);
+                const u4x kp1 = *reinterpret_cast<const u4x *>(&kpart[32 * kb + 16 * hh + 8 + 4 * g2]);
 #pragma unroll
                 for (int e2 = 0; e2 < 4; ++e2) {
                     uint32_t r = pk[e2];
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const int e = 2 * e2 + j;
-                        const int key = k0 + 32 * kb + 16 * hh + 8 * (e >> 2) + 4 * g2 + (e & 3);
-                        const uint32_t h = dropout_mix(hrow ^ dropout_col_term(key));
+                        const int e = 2 * e2 + j;   // key 8*(e >> 2) + 4*g2 + (e & 3) of the 16
+                        const uint32_t h = dropout_mix_tail(rpart ^ ((e >> 2) ? kp1[e & 3] : kp0[e & 3]), thi);
                         if (j == 0 && DMASK)
                             asm("v_cmp_le_u32 vcc, %3, %2\n\t"
                                 "v_cndmask_b32_sdwa %0, 0, %0, vcc dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE "
