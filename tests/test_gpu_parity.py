@@ -329,6 +329,38 @@ def test_config3_buckets(fa, S):
     _check_sampled_heads(fa, f"config3-{S}", q, k, v, do, [(0, 0), (q.shape[0] - 1, 11)])
 
 
+@pytest.mark.parametrize("B,H,S", [(64, 12, 512), (26, 16, 512), (26, 16, 1024), (31, 12, 1050)])
+def test_every_head_written_and_correct(fa, B, H, S):
+    """Short sequences with B*H a multiple of 8 run the forward and dQ pass in groups of 16 heads per
+    XCD (the last group smaller when B*H/8 is not a multiple of 16: 26*16/8 = 52 heads); B*H = 372
+    keeps the plain order.  Outputs start as NaN and every head of every output must be written and
+    match SDPA MATH fp32 on the GPU."""
+    say(f"case every head B={B} H={H} S={S}")
+    lib = capi.load()
+    q, k, v, do = rand_inputs(B, H, S, seed=S + H)
+    o, dq, dk, dv = (torch.full_like(q, float("nan")) for _ in range(4))
+    lse = torch.full((B, H, S), float("nan"), device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    pf = capi.fwd_params(q, k, v, o, lse, 0.125)
+    assert lib.fa2_fwd_f16(ctypes.byref(pf), stream) == 0, lib.fa2_last_error()
+    ws = torch.full((lib.fa2_bwd_workspace_bytes(B, H, S) // 4,), float("nan"), device=DEV)
+    pb = capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, 0.125)
+    assert lib.fa2_bwd_f16(ctypes.byref(pb), 7, ws.data_ptr(), ws.numel() * 4, stream) == 0, lib.fa2_last_error()
+    torch.cuda.synchronize()
+    for name, t in zip(("o", "lse", "dq", "dk", "dv"), (o, lse, dq, dk, dv)):
+        assert torch.isfinite(t).all(), f"{name}: unwritten or non-finite entries"
+    ro, rlse, rdq, rdk, rdv = (torch.from_numpy(x) for x in sdpa_ref_gpu(q, k, v, do))
+    eo = (o.double().cpu() - ro).abs().amax(dim=(2, 3))          # per head
+    el = (lse.double().cpu() - rlse).abs().amax(dim=2)
+    say(f"every head: O max-abs {eo.max().item():.2e}, LSE max-abs {el.max().item():.2e}")
+    assert eo.max().item() <= O_TOL and el.max().item() <= LSE_TOL
+    for name, got, want in (("dQ", dq, rdq), ("dK", dk, rdk), ("dV", dv, rdv)):
+        g = got.double().cpu()
+        e = ((g - want).norm(dim=(2, 3)) / want.norm(dim=(2, 3)).clamp_min(1e-30))   # per head
+        say(f"every head: {name} rel (worst head) {e.max().item():.2e}")
+        assert e.max().item() <= G_TOL, name
+
+
 def test_config4_outlier_rows(fa):
     say("case config 4 B=8 H=16 S=4096 with x8 rows")
     q, k, v, do = wl.config_inputs(4, device=DEV)

@@ -218,6 +218,7 @@ static int fwd_common(const fa2_fwd_params *p, int32_t s_k, int32_t coff, void *
     a.inv_keep = 1.f / (1.f - p->dropout_p);
     const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
     a.drop_mask = dropout ? p->dropout_mask : nullptr;
+    a.hgroup = 0;
     const hipStream_t st = (hipStream_t)stream;
     const hipError_t e = (inference && p->S == 1 && !dropout) ? fa2::launch_fwd_decode(a, causal, st)
                          : nsplit > 1                         ? fa2::launch_fwd_split(a, causal, dropout, st)
@@ -330,6 +331,7 @@ static int bwd_run(const fa2_bwd_params *p, int32_t mode, void *workspace, void 
     a.inv_keep = 1.f / (1.f - p->dropout_p);
     const bool causal = p->causal != 0, dropout = p->dropout_p > 0.f;
     a.drop_mask = dropout ? p->dropout_mask : nullptr;
+    a.hgroup = 0;
     const hipStream_t st = (hipStream_t)stream;
 
     hipError_t e = hipSuccess;

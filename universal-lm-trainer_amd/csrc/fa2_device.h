@@ -150,6 +150,17 @@ __device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, void *
         : "v"(off), "s"(sb), "s"(lds));
 }
 
+// s * v for s, v < 2^24 with the product below 2^32 (v_mul_u32_u24, a
+// full-rate instruction; s wave-uniform).  Written as assembly: from the
+// same product in C the compiler forms v_mad_u64_u32, a quarter-rate
+// instruction, which in per-tile address arithmetic costs more than the
+// rest of that arithmetic together.
+__device__ __forceinline__ uint32_t mul_u24(uint32_t s, uint32_t v) {
+    uint32_t r;
+    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "s"(s), "v"(v));
+    return r;
+}
+
 // LDS byte address of a __shared__ object, for the forms below that take the
 // destination as an integer (converted once, outside the tile loop, instead
 // of a generic-to-LDS pointer conversion at every transfer).
@@ -409,6 +420,31 @@ __device__ __forceinline__ int64_t dmask_word(bool causal, int bh, int S, int t6
     const int64_t J = dmask_tiles(S) >> 1, j = t64 >> 1, n = R - 128 * j;
     const int64_t head = 4 * J * R - 256 * J * (J - 1), before = 4 * j * R - 256 * j * (j - 1);
     return (int64_t)bh * head + before + (int64_t)(t64 & 1) * 2 * n + (int64_t)g2 * n + (q - 128 * j);
+}
+
+// Workgroup order of the query-block kernels (forward, dQ pass): workgroup L
+// of a grid of nq * BH -> its query slot (0 = the head's last, heaviest
+// query block) and its head bh.  Workgroups go to the 8 XCDs in turn
+// (L % 8), each XCD with its own L2.
+//   * G = 0: query slots outermost, heads fastest.  With BH a multiple of 8
+//     a head's workgroups share one XCD, heaviest first over the whole grid,
+//     but BH workgroups apart in time.
+//   * G > 0 (the host passes it only when BH is a multiple of 8): XCD x takes
+//     the heads x + 8 y and runs them in groups of G heads, query slots
+//     heaviest first within each group, so that the query blocks of a head
+//     run at about the same time and share its K / V tiles in the XCD's L2.
+__device__ __forceinline__ void query_block_order(int L, int BH, int nq, int G, int &qslot, int &bh) {
+    if (G > 0) {
+        const int xcd = L & 7, i = L >> 3;
+        const int per = G * nq;                       // workgroups of a full group
+        const int grp = i / per, r = i - grp * per;
+        const int gsz = min(G, (BH >> 3) - grp * G);  // the last group may be smaller
+        qslot = r / gsz;
+        bh = 8 * (grp * G + r - qslot * gsz) + xcd;
+    } else {
+        qslot = L / BH;
+        bh = L - qslot * BH;
+    }
 }
 
 }  // namespace fa2

@@ -31,6 +31,8 @@ struct FwdArgs {
     float inv_keep;      // 1 / (1 - p)
     // Dropout keep bits (dmask_word layout) written for the backward, or null.
     uint32_t *drop_mask;
+    // Workgroup order (query_block_order): heads per group, 0 = plain order.
+    int hgroup;
 };
 
 struct BwdArgs {
@@ -60,6 +62,8 @@ struct BwdArgs {
     const uint32_t *drop_mask;
     // dK/dV pass: one workgroup runs key blocks j and nkb - 1 - j (causal).
     bool dkv_pair;
+    // dQ pass workgroup order (query_block_order): heads per group, 0 = plain.
+    int hgroup;
 };
 
 struct RopeArgs {
