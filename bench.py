@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the parity gate (profiling runs)")
     ap.add_argument("--no-dropout", action="store_true", help="skip the dropout p=0.1 timings")
+    ap.add_argument("--no-power", action="store_true",
+                    help="skip the socket-power readings (amdsmi) over each kernel, the step and a GEMM")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the secondary block that measures every other benchmark configuration "
                          "(3 at S=512..4096, 4, trainer buckets S=4050 and S=1050, 5)")
@@ -104,7 +106,8 @@ class ClockSampler:
     window.  Its wave holds a few registers of one SIMD, which keeps one
     attention workgroup of 512 off that CU meanwhile; steps running beside it
     take ~6% longer, so it runs beside extra steps, never the timed ones.  (amdsmi's gpu_metrics
-    on these boxes do not update under load, so they are not used.)"""
+    give the firmware's view -- current_gfxclk and socket power -- which power_draw reports beside
+    it; its average-clock fields read N/A or stale values on these boxes.)"""
 
     def __init__(self, torch, window_s):
         import ctypes as ct
@@ -154,6 +157,118 @@ def clock_over_steps(torch, step, ms_per_step, n=10):
             step()
     out = clock.report()
     out["sample"] = f"{n} further steps after the timed ones, the probe running beside them"
+    return out
+
+
+def power_draw(torch, calls, seconds=1.5):
+    """Socket power and shader clock while each callable runs back to back:
+    amdsmi's gpu_metrics (current_socket_power, current_gfxclk and the
+    per-XCD clocks), sampled every 50 ms from a host thread over `seconds` of
+    calls after 0.3 s of untimed ones, medians reported; plus the power cap
+    and the energy per executed flop (socket power x time per call / flops).
+    calls: {name: (fn, executed_flops or None)}.  Read-only monitoring."""
+    import threading
+    try:
+        import amdsmi
+        amdsmi.amdsmi_init()
+        handle = amdsmi.amdsmi_get_processor_handles()[0]
+        cap_w = amdsmi.amdsmi_get_power_cap_info(handle)["power_cap"] / 1e6
+    except Exception as e:   # no amdsmi or no device: report why, measure nothing
+        return {"error": f"amdsmi unavailable: {e}"}
+
+    def sample():
+        m = amdsmi.amdsmi_get_gpu_metrics_info(handle)
+        clks = [x for x in (m.get("current_gfxclks") or []) if isinstance(x, int) and 0 < x < 10000]
+        return m.get("current_socket_power"), m.get("current_gfxclk"), clks
+
+    stream = torch.cuda.current_stream()
+    out = {"cap_w": cap_w, "source": "amdsmi gpu_metrics current_socket_power / current_gfxclk, medians of "
+                                      f"50 ms samples over {seconds} s of back-to-back calls"}
+    for name, (fn, flops) in calls.items():
+        samples, stop = [], [False]
+
+        def poll():
+            while not stop[0]:
+                try:
+                    samples.append(sample())
+                except Exception:
+                    pass
+                time.sleep(0.05)
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.3:
+            fn()
+            torch.cuda.synchronize()
+        th = threading.Thread(target=poll)
+        th.start()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 0
+        e0.record(stream)
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+            if n % 16 == 0:
+                torch.cuda.synchronize()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        stop[0] = True
+        th.join()
+        ms = e0.elapsed_time(e1) / n
+        pw = [s[0] for s in samples if isinstance(s[0], (int, float))]
+        ck = [s[1] for s in samples if isinstance(s[1], (int, float))]
+        xcd = [c for s in samples for c in s[2]]
+        r = {"ms_per_call": round(ms, 4), "socket_w": statistics.median(pw) if pw else None,
+             "gfxclk_mhz": statistics.median(ck) if ck else None,
+             "xcd_gfxclk_mhz": [min(xcd), max(xcd)] if xcd else None, "samples": len(samples)}
+        if flops and pw:
+            r["tflops"] = round(flops / (ms / 1e3) / 1e12, 1)
+            r["pj_per_flop"] = round(statistics.median(pw) * ms / 1e3 / flops * 1e12, 3)
+        out[name] = r
+    return out
+
+
+def power_block(torch, q, k, v, do, B, H, S):
+    """power_draw over the three kernels through the C ABI (preallocated
+    outputs), the whole step, and for comparison torch's fp16 GEMM at 8192^3
+    (hipBLASLt), the chip's dense-MFMA reference under the same power cap."""
+    import fa2_capi
+    lib = fa2_capi.load()
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device="cuda")
+    dq, dk, dv = (torch.empty(B, H, S, 64, dtype=torch.float16, device="cuda") for _ in range(3))
+    ws = torch.empty(lib.fa2_bwd_workspace_bytes(B, H, S) // 4 + 64, device="cuda")
+    pf = fa2_capi.fwd_params(q, k, v, o, lse, 0.125)
+    pb = fa2_capi.bwd_params(q, k, v, o, lse, do, dq, dk, dv, 0.125)
+    nb = ws.numel() * 4
+
+    def fwd():
+        return lib.fa2_fwd_f16(ctypes.byref(pf), sp)
+
+    def bdq():
+        return lib.fa2_bwd_f16(ctypes.byref(pb), 2, ws.data_ptr(), nb, sp)
+
+    def bdkv():
+        return lib.fa2_bwd_f16(ctypes.byref(pb), 4, ws.data_ptr(), nb, sp)
+
+    def step():
+        fwd()
+        bdq()
+        bdkv()
+    for f in (fwd, bdq, bdkv):
+        assert f() == 0, lib.fa2_last_error()
+    ga = torch.randn(8192, 8192, device="cuda", dtype=torch.float16)
+    gb = torch.randn(8192, 8192, device="cuda", dtype=torch.float16)
+    unit = B * H * S * S * 64
+    calls = {"fwd": (fwd, 2 * unit), "bwd_dq": (bdq, 3 * unit), "bwd_dkv": (bdkv, 4 * unit),
+             "step": (step, 9 * unit), "gemm_8192_fp16": (lambda: torch.matmul(ga, gb), 2 * 8192 ** 3)}
+    out = power_draw(torch, calls)
+    st = out.get("step", {})
+    if st.get("socket_w"):
+        out["step_pj_per_algorithmic_flop"] = round(st["socket_w"] * st["ms_per_call"] / 1e3 / (7 * unit) * 1e12, 3)
+    out["flops"] = "executed: fwd 2, dQ pass 3, dK/dV pass 4, step 9 units of B*H*S^2*D; algorithmic step 7"
+    del o, lse, dq, dk, dv, ws, ga, gb
     return out
 
 
@@ -711,6 +826,7 @@ def main():
         case["timing"]["dropout"] = dropout_steps(torch, ext, q, k, v, do, 0.125, torch.cuda.current_stream(),
                                                   step_flops)
     case["timing"]["rope"] = rope_timing(torch, ext, B, H, S, torch.cuda.current_stream())
+    power = None if args.no_power else power_block(torch, q, k, v, do, B, H, S)
     del q, k, v, do
     torch.cuda.empty_cache()
 
@@ -739,6 +855,8 @@ def main():
         "clock": case["clock"],
         "parity": case["parity"],
     }
+    if power is not None:
+        result["power"] = power
     if not args.no_configs and args.config == "2":
         result["configs"] = configs_block(args, torch, fa, ext)
     if not args.no_cpu:
