@@ -116,6 +116,10 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
     // DMASK: per stage and wave, the words of its 64 queries (32 when NARROW)
     // for halves g2 = 0, 1.
     __shared__ __attribute__((aligned(16))) uint32_t sMQ[DMASK ? NSK : 1][DQ_NW][2][64];
+    // Each lane's four transfer offsets of a full tile (K rows i = 0, 1, then
+    // V rows), 1 KB per wave.
+    typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) u4x sOff[DQ_NW * 64];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -157,9 +161,12 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
     // chunk position 64j + L = 8*row + (L & 7), row = 8j + (L >> 3), and
     // fetches logical chunk (L & 7) ^ swz_both(row) of key row k0 + row (rows
     // past S: row S - 1, masked on use).
-    // Offsets are recomputed for every tile from the lane index, re-read
-    // through an opaque move so that nothing derived from it stays live
-    // across the tile loop: a few VALU operations per tile save registers.
+    // The offsets of a full tile are fixed: computed once, kept in an LDS
+    // slot of the wave and read back with one ds_read_b128 per tile (the
+    // kernel has no registers to hold them across the loop; recomputing them
+    // every tile cost ~25 VALU instructions).  The last, partial tile
+    // recomputes them from the lane index, re-read through an opaque move so
+    // that nothing derived from it stays live across the tile loop.
     auto tile_offsets = [&](int k0, uint32_t(&ko)[2], uint32_t(&vo)[2]) FA2_INLINE {
         int ln;
         asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
@@ -184,9 +191,28 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
     // DMASK: the wave's 64 (NARROW: 32) words per half g2 of each tile (rows
     // past S are within the mask's padded rows), 4 bytes per lane.
     const uint32_t lds_mq = lds_addr(&sMQ[0][wave][0][0]);
+    {
+        // (With S < DQ_KT every tile is partial and recomputes its offsets,
+        // so the clamped values stored then go unread.)
+        uint32_t ko[2], vo[2];
+        tile_offsets(0, ko, vo);
+        sOff[64 * wave + lane] = u4x{ko[0], ko[1], vo[0], vo[1]};
+    }
     auto issue_next = [&]() FA2_INLINE {
         uint32_t ko[2], vo[2];
-        tile_offsets(kn, ko, vo);
+        if (kn + DQ_KT > S) {
+            tile_offsets(kn, ko, vo);
+        } else {
+            // An opaque slot address: the read stays in the loop instead of
+            // being hoisted into four live registers.
+            uint32_t oa = lds_addr(&sOff[64 * wave]) + 16u * (uint32_t)lane;
+            asm volatile("" : "+v"(oa));
+            const u4x ov = *reinterpret_cast<const __attribute__((address_space(3))) u4x *>(oa);
+            ko[0] = ov[0];
+            ko[1] = ov[1];
+            vo[0] = ov[2];
+            vo[1] = ov[3];
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint32_t d = lds_kv + stn * (uint32_t)sizeof(sKV[0]) + 1024u * (uint32_t)i;

@@ -104,6 +104,10 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     // Dropout: per wave, the column part dropout_xs16(col term) of the
     // current tile's KT keys, formed once per key and read by every lane.
     __shared__ __attribute__((aligned(16))) uint32_t sDK[DROPOUT ? NW * KT : 1];
+    // NARROW: each lane's four transfer offsets of a full tile (K rows i = 0,
+    // 1, then V rows), 1 KB per wave.
+    typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) u4x sOff[NARROW ? NW * 64 : 1];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
@@ -174,10 +178,12 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     // key row k0 + row.  The lane's byte offsets within a tile are fixed; only
     // the last tile, whose rows past Sk are redirected to row Sk - 1 (any
     // finite row: their scores are masked and their P is zero), needs them
-    // recomputed.  The narrow variant recomputes them for every tile from the
-    // lane index, re-read through an opaque move so that nothing derived from
-    // it stays live across the tile loop: a few VALU operations per tile save
-    // the registers that let four waves share a SIMD.
+    // recomputed.  The narrow variant, whose four waves per SIMD leave no
+    // registers to hold them across the tile loop, keeps them in an LDS slot
+    // of the wave and reads them back with one ds_read_b128 per tile (its
+    // last, partial tile recomputes them from the lane index, re-read through
+    // an opaque move so that nothing derived from it stays live across the
+    // loop).  Recomputing every tile cost ~25 VALU instructions per tile.
     auto tile_offsets = [&](int k0, uint32_t(&ko)[2], uint32_t(&vo)[2]) FA2_INLINE {
         int ln = lane;
         if (NARROW) asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
@@ -194,7 +200,15 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     // Stage of tile t (t >= 0; unsigned, so a power-of-two count is a mask).
     auto stage_of = [](int t) FA2_INLINE { return (int)((uint32_t)t % (uint32_t)NSK); };
     uint32_t koffg[2] = {0u, 0u}, voffg[2] = {0u, 0u};
-    if (!NARROW) tile_offsets(0, koffg, voffg);
+    if (!NARROW) {
+        tile_offsets(0, koffg, voffg);
+    } else {
+        // A full tile's offsets (with Sk < KT every tile is partial and
+        // recomputes them, so the clamped values stored then go unread).
+        uint32_t ko[2], vo[2];
+        tile_offsets(0, ko, vo);
+        sOff[64 * wave + lane] = u4x{ko[0], ko[1], vo[0], vo[1]};
+    }
     // Tiles are issued in order, once each: issue_next() sends the next tile
     // (the callers' index tests only decide whether there is one).  Scalar
     // running addresses (global tile bases, LDS stage) advance by a constant
@@ -208,7 +222,19 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     const uint32_t lds_kv = lds_addr(&sKV[0][0][0]) + 1024u * (uint32_t)(TPW * wave);
     auto issue_next = [&]() FA2_INLINE {
         uint32_t ko[2] = {koffg[0], koffg[1]}, vo[2] = {voffg[0], voffg[1]};
-        if (NARROW || kn + KT > Sk) tile_offsets(kn, ko, vo);
+        if (kn + KT > Sk) {
+            tile_offsets(kn, ko, vo);
+        } else if (NARROW) {
+            // An opaque slot address: the read stays in the loop instead of
+            // being hoisted into four live registers.
+            uint32_t oa = lds_addr(&sOff[64 * wave]) + 16u * (uint32_t)lane;
+            asm volatile("" : "+v"(oa));
+            const u4x ov = *reinterpret_cast<const __attribute__((address_space(3))) u4x *>(oa);
+            ko[0] = ov[0];
+            ko[1] = ov[1];
+            vo[0] = ov[2];
+            vo[1] = ov[3];
+        }
 #pragma unroll
         for (int i = 0; i < TPW; ++i) {
             const uint32_t d = lds_kv + stn * (uint32_t)sizeof(sKV[0]) + 1024u * (uint32_t)i;
