@@ -531,9 +531,8 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
     // One tile of the in-order loops: scores, masking, softmax (with its cold
     // path on the live scores), dropout, P V; returns the keep word of query
     // block 0 (DMASK).
-    auto inorder_tile = [&](int t, f16x(&s)[QB][2], h8(&p)[QB][2][2]) FA2_INLINE -> uint32_t {
+    auto inorder_tile = [&](int t, int stage, f16x(&s)[QB][2], h8(&p)[QB][2][2]) FA2_INLINE -> uint32_t {
         const int k0 = kbase + t * KT;
-        const int stage = stage_of(t);
         uint32_t w = 0;
         s_mm(stage, s);
         if (need_mask(k0)) {
@@ -592,17 +591,28 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
         lds_barrier();                         // tile 0 landed for every wave
         f16x s[QB][2];
         h8 p[QB][2][2];
-        for (int t = 0; t < ntiles; ++t) {
-            uint32_t w = 0;
-            if (t <= tlast) w = inorder_tile(t, s, p);
-            if (t + 1 < ntiles) {
-                wait_tiles(min(NSK - 2, ntiles - 2 - t));   // tile t+1 landed
-                lds_barrier();
-                if (t + NSK < ntiles) issue_next();
-            }
-            if (DMASK && t <= tlast) {
-                const int q = qw0 + c;   // QB == 1
-                if (q < S) a.drop_mask[dmask_word(CAUSAL, bh, S, kbase / KT + t, g2, q)] = w;
+        // Unrolled over the NSK stages (tile t sits in stage t % NSK, and
+        // every wave starts at tile 0), so that each copy's stage is a
+        // constant and the operand reads address LDS through instruction
+        // offsets, with no per-tile address arithmetic.  (With keep-bit
+        // words the copies would spill: one copy, the stage at run time.)
+        constexpr int U = DMASK ? 1 : NSK;
+        for (int t0 = 0; t0 < ntiles; t0 += U) {
+#pragma unroll
+            for (int ph = 0; ph < U; ++ph) {
+                const int t = t0 + ph;
+                if (t >= ntiles) break;
+                uint32_t w = 0;
+                if (t <= tlast) w = inorder_tile(t, U == 1 ? stage_of(t) : ph, s, p);
+                if (t + 1 < ntiles) {
+                    wait_tiles(min(NSK - 2, ntiles - 2 - t));   // tile t+1 landed
+                    lds_barrier();
+                    if (t + NSK < ntiles) issue_next();
+                }
+                if (DMASK && t <= tlast) {
+                    const int q = qw0 + c;   // QB == 1
+                    if (q < S) a.drop_mask[dmask_word(CAUSAL, bh, S, kbase / KT + t, g2, q)] = w;
+                }
             }
         }
         vm_wait<0>();
@@ -624,7 +634,7 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
         f16x s[QB][2];
         h8 p[QB][2][2];
         for (int t = 0; t < ntiles; ++t) {
-            if (t <= tlast) (void)inorder_tile(t, s, p);
+            if (t <= tlast) (void)inorder_tile(t, stage_of(t), s, p);
             if (!(t & 1) && t + 1 < ntiles) continue;   // the pair's first tile
             vm_wait<0>();                                // tiles t+1, t+2 (the next pair) landed
             lds_barrier();                               // every wave is done with tiles t-1, t
