@@ -357,9 +357,15 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
         if (NSK - 1 < ntiles) issue_next();   // the last stage's tile (the prologue sent the others)
         wait_tiles(min(NSK - 1, ntiles - 1));
         lds_barrier();                         // tile 0 landed for every wave
-        for (int t = 0; t < ntiles; ++t) {
+        // Unrolled over the NSK stages (every wave starts at tile 0 and tile t
+        // sits in stage t % NSK), so that each copy's stage is a constant and
+        // the operand reads address LDS through instruction offsets.
+        for (int t0 = 0; t0 < ntiles; t0 += NSK) {
+#pragma unroll
+          for (int st = 0; st < NSK; ++st) {
+            const int t = t0 + st;
+            if (t >= ntiles) break;
             if (t <= tlast) {
-                const int st = stage_of(t);
                 const bool m = need_mask(t);
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
@@ -389,6 +395,7 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
                 lds_barrier();
                 if (t + NSK < ntiles) issue_next();
             }
+          }
         }
         vm_wait<0>();
         lds_barrier();   // every wave is done with the stages: the dQ staging reuses them
@@ -409,8 +416,12 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
         };
         wait_pending(min(NSK - 2, ntiles - 2));   // tiles 0 and 1 landed
         lds_barrier();
-        for (int t = 0; t < ntiles; ++t) {
-            const int st = stage_of(t);
+        // Unrolled over the four stages, as in the narrow loop.
+        for (int t0 = 0; t0 < ntiles; t0 += NSK) {
+#pragma unroll
+          for (int st = 0; st < NSK; ++st) {
+            const int t = t0 + st;
+            if (t >= ntiles) break;
             if (t <= tlast) {
                 const bool m = need_mask(t);
 #pragma unroll
@@ -454,6 +465,7 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
                 if (t + 3 < ntiles) issue_next();
                 if (t + 4 < ntiles) issue_next();
             }
+          }
         }
     }
 
