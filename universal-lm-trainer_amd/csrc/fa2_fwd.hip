@@ -542,11 +542,29 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
         }
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            float rs = p_form(s[qb], msc[qb], p[qb]);
+            float rs;
+            if (!DMASK && t == 0) {
+                // First tile: msc is -inf, so P against it would only fail
+                // the overflow check into the cold path (a second P pass).
+                // Take the row max from the live scores directly, as the
+                // cold path would (with O and l still zero its rescale is a
+                // no-op), so the result is the same bits; -inf when every key
+                // is masked.  (With keep-bit words this copy would spill;
+                // they keep the cold path, with the same result.)
+                float mx = s[qb][0][0];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
+                mx = fmaxf(mx, xor32(mx)) * scale2;
+                msc[qb] = mx;
+                rs = p_form(s[qb], (mx == -INFINITY) ? 0.f : mx, p[qb]);
+            } else {
+                rs = p_form(s[qb], msc[qb], p[qb]);
+            }
             if (__any(!(rs <= P_SUM_LIMIT))) {
                 // The cold path on the live scores: true row max, rescale of
-                // O and l, P again (on the first tile msc is -inf and it
-                // always runs).
+                // O and l, P again (almost never after the first tile).
                 FA2_COLD_BRANCH();
                 float mx = s[qb][0][0];
 #pragma unroll
