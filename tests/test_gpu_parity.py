@@ -115,9 +115,10 @@ def test_softmax_scales(fa, scale):
 
 @pytest.mark.parametrize("scale,amp,S", [(1.0, 4.0, 97), (0.125, 4.0, 250), (1e-3, 1.0, 130), (1e-25, 1.0, 70)])
 def test_row_term_extremes(fa, scale, amp, S):
-    """Large logits (LSE up to ~10^2 in log2 units, so -LSE*log2e/scale2 is large) and tiny scales: the
-    dK/dV pass adds the row terms through bf16 MFMA steps for scale2 >= 1e-20 and subtracts them
-    per element below that (the 1e-25 case); S not a multiple of 32 exercises the last term block."""
+    """Large logits (LSE up to ~10^2 in log2 units, so -LSE*log2e/scale2 is large) and tiny scales:
+    without dropout the dK/dV pass starts its S and dP chains at the row terms -LSE*log2e/scale2 and
+    -delta for scale2 >= 1e-20, and subtracts them per element below that (the 1e-25 case); S not a
+    multiple of 32 exercises the last term block."""
     say(f"case row terms scale={scale} amp={amp} S={S}")
     q, k, v, do = rand_inputs(1, 2, S, seed=31)
     q, k = (q.float() * amp).half(), (k.float() * amp).half()
@@ -143,6 +144,25 @@ def test_dropout_vs_oracle(fa, p, seed):
     # it, so the O bar does too (grads keep the relative bar).
     check_against(f"dropout p={p}", got, oracle_ref(q, k, v, do, True, 0.125, p=p, seed=seed),
                   o_tol=O_TOL / (1.0 - p))
+
+
+@pytest.mark.parametrize("scale,causal", [(0.125, True), (1.0, True), (-0.3, False), (1.0, False)])
+def test_dropout_scales(fa, scale, causal):
+    """Dropout at the scales the other dropout tests leave out (1.0, where scale*log2(e) > 1, and a
+    negative one, which negates an operand), causal and not: with the forward's keep-bit words and
+    with the hash, against the oracle, and the two bitwise equal."""
+    p, seed = 0.1, 0xD0
+    say(f"case dropout scale={scale} causal={causal}")
+    ext = fa.extension()
+    q, k, v, do = rand_inputs(1, 2, 190, seed=19)
+    o, lse, mask = ext.fa_fwd_mask(q, k, v, p, causal, scale, seed)
+    words = ext.fa_bwd(q, k, v, o, lse, do, p, causal, scale, seed, 7, mask=mask)
+    hashed = ext.fa_bwd(q, k, v, o, lse, do, p, causal, scale, seed, 7)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dQ", "dK", "dV"), words, hashed):
+        assert torch.equal(a, b), f"{name}: keep words and hash differ"
+    check_against(f"dropout scale={scale} causal={causal}", (o, lse, *words),
+                  oracle_ref(q, k, v, do, causal, scale, p=p, seed=seed), o_tol=O_TOL / (1.0 - p))
 
 
 def test_medium_vs_sdpa_math_gpu(fa):
