@@ -135,6 +135,19 @@ def test_row_term_extremes(fa, scale, amp, S):
     assert orc.rel_l2(dv, np.asarray(ref[4], np.float64)) <= G_TOL
 
 
+@pytest.mark.parametrize("S", [160, 1100])
+def test_subnormal_output_gradient(fa, S):
+    """dO of order 1e-4, so that about half its fp16 values are subnormal: delta = rowsum(O * dO) and
+    everything downstream must keep them (a flush to zero would bias delta and every dS); S = 1100
+    takes the two-block dQ pass, S = 160 the narrow one."""
+    say(f"case subnormal dO S={S}")
+    q, k, v, do = rand_inputs(1, 2, S, seed=23)
+    do = (do.float() * 1e-4).half()
+    assert (do.abs() < 2.0 ** -14).float().mean().item() > 0.3
+    got = run_kernel(fa, q, k, v, do)
+    check_against(f"subnormal dO S={S}", got, oracle_ref(q, k, v, do, True, 0.125))
+
+
 @pytest.mark.parametrize("p,seed", [(0.1, 1), (0.5, 0xC0FFEE), (0.9, 42)])
 def test_dropout_vs_oracle(fa, p, seed):
     say(f"case dropout p={p} seed={seed}")

@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256, NARROW ? DQ_NARROW_WAVES : 2) void bwd_dq_pipe
             const h8 qv = *reinterpret_cast<const h8 *>(Qp + (int64_t)qr * a.qss + d0);
             const h8 dv = *reinterpret_cast<const h8 *>(dOp + (int64_t)qr * a.doss + d0);
             const h8 ov = *reinterpret_cast<const h8 *>(Op + (int64_t)qr * a.oss + d0);
-            qf[qb][st] = a.negate ? neg_h8(qv) : qv;
+            qf[qb][st] = neg_h8_if(qv, a.negate);
             dof[qb][st] = dv;
 #pragma unroll
             for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)dv[e];
@@ -569,7 +569,7 @@ __device__ __forceinline__ void dkv_block(const BwdArgs &a, const int kblk, cons
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             const h8 kv = *reinterpret_cast<const h8 *>(krow + 16 * st);
-            kf[st] = a.negate ? neg_h8(kv) : kv;
+            kf[st] = neg_h8_if(kv, a.negate);
             vf[st] = *reinterpret_cast<const h8 *>(vrow + 16 * st);
         }
     }

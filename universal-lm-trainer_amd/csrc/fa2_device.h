@@ -274,9 +274,14 @@ __device__ __forceinline__ h8 acc_to_h8(const f16x &acc, int hh) {
     return __builtin_convertvector(x, h8);
 }
 
-// Flip the sign of all eight halves (exact); used to fold a negative softmax
-// scale into one operand.
-__device__ __forceinline__ h8 neg_h8(h8 v) { return -v; }
+// Flips the sign of all eight halves when `neg` (exact), used to fold a
+// negative softmax scale into one operand: one xor per register with both
+// halves' sign bits, where the fp16 negation and a select took four
+// instructions per register.
+__device__ __forceinline__ h8 neg_h8_if(h8 v, bool neg) {
+    typedef uint32_t u4w __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(h8, __builtin_bit_cast(u4w, v) ^ (neg ? 0x80008000u : 0u));
+}
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
 

@@ -167,7 +167,7 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             const h8 v = *reinterpret_cast<const h8 *>(qrow + 16 * st);
-            qf[qb][st] = a.negate ? neg_h8(v) : v;
+            qf[qb][st] = neg_h8_if(v, a.negate);
         }
     }
 
@@ -915,7 +915,7 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_kernel(const FwdArgs a) {
     const _Float16 *Kp = a.k + b * a.ksb + h * a.ksh + 8 * c8;
     const _Float16 *Vp = a.v + b * a.vsb + h * a.vsh + 8 * c8;
     const h8 qv = *reinterpret_cast<const h8 *>(a.q + b * a.qsb + h * a.qsh + 8 * c8);
-    const h8 qn = a.negate ? neg_h8(qv) : qv;
+    const h8 qn = neg_h8_if(qv, a.negate);
     const float scale2 = a.scale2;
 
     float m = -INFINITY, l = 0.f;
