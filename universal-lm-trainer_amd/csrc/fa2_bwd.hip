@@ -10,12 +10,12 @@
 //
 // dQ accumulation: split pass, like the reference (its dQ and dK/dV kernels,
 // bwd.cu:66-428), with no atomics:
-//   * bwd_dq_pipe_kernel: a workgroup owns 256 queries, keeps Q^T, dO^T, lse
-//     and delta of its queries in registers and streams key tiles (K, V
-//     row-major via LDS; K^T operands come from transposing ds_read_b64_tr_b16
-//     reads), in order, three tiles in flight.  It also computes delta itself (the reference's pre-pass,
-//     bwd.cu:42-61) from the O and dO rows it holds and stores it for the
-//     dK/dV pass.  S^T and dP^T accumulators give each lane one query, so
+//   * bwd_dq_pipe_kernel: a workgroup owns 256 queries (128 for S <= 1024),
+//     keeps Q^T, dO^T, lse and delta of its queries in registers and streams
+//     key tiles (K, V row-major via LDS; K^T operands come from transposing
+//     ds_read_b64_tr_b16 reads) in order.  It also computes delta itself (the
+//     reference's pre-pass, bwd.cu:42-61) from the O and dO rows it holds and
+//     stores it, with the row terms, for the dK/dV pass.  S^T and dP^T accumulators give each lane one query, so
 //     lse/delta are per-lane scalars and dS^T feeds the dQ^T = K^T dS^T MFMA
 //     straight from registers.
 //   * bwd_dkv_pipe_kernel: a workgroup owns 128 keys (32 per wave, K^T and
@@ -80,17 +80,18 @@ constexpr int DQ_NW = 4;
 constexpr int DQ_QB = 2;                    // 32-query blocks per wave
 constexpr int DQ_KT = 64;                   // keys per tile
 constexpr int DQ_QWG = DQ_NW * 32 * DQ_QB;  // 256 queries per workgroup
-constexpr int QP_NST = 4;   // LDS stages: key tile t read, t+1 .. t+3 in flight
+constexpr int QP_NST = 4;   // LDS stages: a pair of key tiles read, the next pair in flight
 
 // 256 queries per workgroup, 64 per wave (two 32-query blocks), 64-key tiles
 // taken 32 keys (kb) at a time, in order: S and dP of both query blocks from
 // one pass over the K / V row fragments (each fragment read from LDS feeds two
 // MFMAs), dS, then dQ of both blocks from one pass over the K^T fragments.
 // The loop is not pipelined inside the wave -- the other workgroup's wave on
-// the same SIMD overlaps its matrix and vector work -- so a step reads only
-// its own tile and three tiles stay in flight.  (A pipelined form that
-// interleaved neighbouring 32 x 32 units inside the wave, each reading its
-// fragments itself, was 2% slower at S = 4096 and 4% at S = 512.)
+// the same SIMD overlaps its matrix and vector work.  Tiles go in pairs with
+// one barrier per pair: while two tiles are read, the next two are in
+// flight.  (A pipelined form that interleaved neighbouring 32 x 32 units
+// inside the wave, each reading its fragments itself, was 2% slower at
+// S = 4096 and 4% at S = 512.)
 //
 // DMASK (dropout with a.drop_mask): the keep bits come from the words the
 // forward wrote (two per query and key tile, moved into LDS with the tile)

@@ -8,27 +8,31 @@
 // tiles, causal tiles past the diagonal skipped, the denominator summed from
 // the un-dropped P, O = acc / l with l == 0 -> 0, LSE in natural log.
 //
-// Work decomposition (one workgroup = 4 waves of one (b, h)):
-//   * without dropout or key slices (the training path at p = 0 and most
-//     inference calls), each wave owns 64 queries, two 32-query blocks: every
-//     K and V operand fragment read from LDS feeds the MFMAs of both blocks,
-//     and the tile loop runs in order (scores, softmax, P V) -- the other
-//     workgroup's wave on the same SIMD overlaps its matrix and vector work;
-//   * with dropout or key slices, each wave owns 32 queries and the tile loop
-//     is software pipelined as described below;
+// Work decomposition (one workgroup = 4 waves of one (b, h)); three loops,
+// chosen per call by launch_fwd_t:
+//   * NARROW (the training shapes, with or without dropout and keep-bit
+//     words, and large prefill chunks): each wave owns one 32-query block,
+//     the tile loop runs in order (scores, softmax, P V) with two LDS stages
+//     (one tile read, one in flight) and one barrier per tile, and at most
+//     128 registers per lane let four workgroups share a CU: the other three
+//     waves of the SIMD cover a wave's latencies;
+//   * two query blocks per wave (smaller grids that still fill two
+//     workgroups per CU, without keep-bit words): every K and V operand
+//     fragment read from LDS feeds the MFMAs of both blocks, the tile loop
+//     runs in order with four stages (one read, three in flight);
+//   * one query block per wave, software pipelined (short query ranges,
+//     key slices): step t issues the P V MFMAs of tile t-1 and the score
+//     MFMAs of tile t+1 while the VALU forms P of tile t, in chunks that pair
+//     two MFMAs with four exponentials; four stages (three resident, one in
+//     flight);
 //   * a wave's Q^T operands (16 x 32 fp16 per d-step and block) stay in
 //     registers for the whole kernel;
 //   * key tiles of 64 keys are moved global -> LDS by the waves' direct
 //     transfers (global_load_lds, no register staging; a scalar tile base
-//     plus fixed 32-bit lane offsets) into XOR-swizzled tiles, four stages
-//     deep (pipelined loop: three resident, one in flight; in-order loop: one
-//     read, three in flight); K feeds the A operand of
-//     S^T = K Q^T with 16-byte reads, V feeds the A operand of O^T = V^T P^T
-//     through transposing ds_read_b64_tr_b16 reads, both free of LDS bank
-//     conflicts;
-//   * the pipelined loop: step t issues the P V MFMAs of
-//     tile t-1 and the score MFMAs of tile t+1 while the VALU forms P of
-//     tile t, in chunks that pair two MFMAs with four exponentials;
+//     plus fixed 32-bit lane offsets) into XOR-swizzled tiles; K feeds the A
+//     operand of S^T = K Q^T with 16-byte reads, V feeds the A operand of
+//     O^T = V^T P^T through transposing ds_read_b64_tr_b16 reads, both free
+//     of LDS bank conflicts;
 //   * S^T accumulators give each lane one query and 32 keys, so the row max
 //     is a local max plus one cross-half exchange, the running sum l stays a
 //     per-lane partial until the epilogue, the O^T rescale is a per-lane
@@ -38,8 +42,6 @@
 //     max and an overflow check on its row sum (v_dot2_f32_f16 on the packed
 //     fp16 P) decides when the true max, the O/l rescale and a recompute are
 //     needed, which is almost never after the first tile;
-//   * at most 256 registers per lane, so two workgroups share each CU and
-//     one's barrier waits are covered by the other's work;
 //   * workgroups are issued heaviest first (last query blocks first) and all
 //     workgroups of one (b, h) share blockIdx % 8, i.e. one XCD and its L2.
 #include "fa2_device.h"
@@ -75,11 +77,12 @@ constexpr float P_SUM_LIMIT = 32768.f;  // per-lane partial sum bound: every P <
 // DMASK (dropout, no key slices): each lane also stores its tile's 32 keep
 // bits as one word of a.drop_mask (dmask_word layout), for the backward.
 //
-// NARROW (one query block per wave): the in-order loop with three LDS stages
-// and one barrier per tile, at most 168 registers per lane, so that three
-// workgroups (three waves per SIMD) share a CU: with one query block a wave's
-// scores -> softmax -> P V chain is short, and a third wave covers its
-// latencies.
+// NARROW (one query block per wave): the in-order loop with one barrier per
+// tile and, by default (NARROW_WAVES = 4), two LDS stages and at most 128
+// registers per lane, so that four workgroups (four waves per SIMD) share a
+// CU; NARROW_WAVES = 3 gives three stages and 168 registers.  With one query
+// block a wave's scores -> softmax -> P V chain is short, and the other waves
+// of the SIMD cover its latencies.
 #ifndef FA2_FWD_NARROW_WAVES
 #define FA2_FWD_NARROW_WAVES 4
 #endif
