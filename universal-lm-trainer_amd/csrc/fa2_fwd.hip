@@ -229,9 +229,19 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
             tile_offsets(kn, ko, vo);
         } else if (NARROW) {
             // An opaque slot address: the read stays in the loop instead of
-            // being hoisted into four live registers.
-            uint32_t oa = lds_addr(&sOff[64 * wave]) + 16u * (uint32_t)lane;
-            asm volatile("" : "+v"(oa));
+            // being hoisted into four live registers.  With keep-bit words
+            // it is formed from an opaque copy of the lane index every tile,
+            // so that no register holds it across the loop (kept live, that
+            // variant spilled it to scratch and reloaded it at every tile).
+            uint32_t oa;
+            if (DMASK) {
+                uint32_t ln;
+                asm volatile("v_mov_b32 %0, %1" : "=v"(ln) : "v"(lane));
+                oa = lds_addr(&sOff[64 * wave]) + 16u * ln;
+            } else {
+                oa = lds_addr(&sOff[64 * wave]) + 16u * (uint32_t)lane;
+                asm volatile("" : "+v"(oa));
+            }
             const u4x ov = *reinterpret_cast<const __attribute__((address_space(3))) u4x *>(oa);
             ko[0] = ov[0];
             ko[1] = ov[1];
@@ -607,6 +617,16 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
             else if (n == 1) vm_wait<2 * TPW>();
             else vm_wait<4 * TPW>();
         };
+#ifndef FA2_FWD_STORE_SLACK
+#define FA2_FWD_STORE_SLACK 0
+#endif
+        // The same with the previous tile's keep-word store (issued after
+        // every transfer being waited for) allowed to stay in flight.
+        auto wait_tiles_st = [&](int n) FA2_INLINE {
+            if (n <= 0) vm_wait<1>();
+            else if (n == 1) vm_wait<2 * TPW + 1>();
+            else vm_wait<4 * TPW + 1>();
+        };
         if (NSK - 1 < ntiles) issue_next();   // the last stage's tile (the prologue sent the others)
         wait_tiles(min(NSK - 1, ntiles - 1));
         lds_barrier();                         // tile 0 landed for every wave
@@ -626,7 +646,10 @@ __global__ __launch_bounds__(NW * 64, NARROW ? NARROW_WAVES : 8 / NW) void fwd_k
                 uint32_t w = 0;
                 if (t <= tlast) w = inorder_tile(t, U == 1 ? stage_of(t) : ph, s, p);
                 if (t + 1 < ntiles) {
-                    wait_tiles(min(NSK - 2, ntiles - 2 - t));   // tile t+1 landed
+                    if (DMASK && FA2_FWD_STORE_SLACK && t >= 1 && t - 1 <= tlast)
+                        wait_tiles_st(min(NSK - 2, ntiles - 2 - t));
+                    else
+                        wait_tiles(min(NSK - 2, ntiles - 2 - t));   // tile t+1 landed
                     lds_barrier();
                     if (t + NSK < ntiles) issue_next();
                 }
