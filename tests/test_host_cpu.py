@@ -364,3 +364,11 @@ def test_bench_step_roofline():
     assert r["minimum"]["bound"] == "hbm" and abs(r["minimum"]["attainable"] - 1188.5) < 0.1
     assert r["split_design"]["algorithmic_bytes"] == 16 * 64 * 12 * 512 * 128 + 8 * 64 * 12 * 512 * 4
     assert abs(r["minimum"]["frac"] - 360.0 / r["minimum"]["attainable"]) < 1e-4
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 exits with a nonzero status and says why."""
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode != 0
+    assert "one GPU only" in r.stdout + r.stderr
