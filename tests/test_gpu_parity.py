@@ -362,12 +362,14 @@ def test_config3_buckets(fa, S):
     _check_sampled_heads(fa, f"config3-{S}", q, k, v, do, [(0, 0), (q.shape[0] - 1, 11)])
 
 
-@pytest.mark.parametrize("B,H,S", [(64, 12, 512), (26, 16, 512), (26, 16, 1024), (31, 12, 1050), (2, 4, 300)])
+@pytest.mark.parametrize("B,H,S", [(64, 12, 512), (26, 16, 512), (26, 16, 1024), (31, 12, 1050), (2, 4, 300),
+                                   (1024, 8, 128), (3, 5, 2100)])
 def test_every_head_written_and_correct(fa, B, H, S):
     """Short sequences with B*H a multiple of 8 run the forward and dQ pass in groups of 16 heads per
     XCD (the last group smaller when B*H/8 is not a multiple of 16: 26*16/8 = 52 heads; one head per
-    XCD at B*H = 8); B*H = 372 keeps the plain order.  Outputs start as NaN and every head of every
-    output must be written and match SDPA MATH fp32 on the GPU."""
+    XCD at B*H = 8); B*H = 372 keeps the plain order; 8192 heads of one 128-query block each give the
+    largest grids; B*H = 15 at S = 2100 takes the pipelined forward and the two-block dQ pass.  Outputs
+    start as NaN and every head of every output must be written and match SDPA MATH fp32 on the GPU."""
     say(f"case every head B={B} H={H} S={S}")
     lib = capi.load()
     q, k, v, do = rand_inputs(B, H, S, seed=S + H)
